@@ -1,0 +1,196 @@
+// Device-side building blocks shared by every EXL3 kernel (gfx950, wave64).
+//
+// Format (reference exl3.h:4-21, exl3.cpp:55-107): one 16x16 tile is 8*K little-endian
+// 32-bit ring words (256*K bits, read MSB first). Stream position p's 16-bit state is
+// the window of ring bits ending (exclusive) at bit (p+1)*K; p = L*8 + i (L = one of
+// 32 "reference lanes") maps to tile element row = 2*(L%4) + {0,1,8,9}[i%4],
+// col = L/4 + 8*(i/4).
+//
+// Lane mapping used by every GEMV here (wave64): a wave works on 8 tiles that are
+// adjacent along n (128 output columns, one Hadamard block) at one k-tile. Eight
+// lanes share a tile; lane m of a tile holds that tile's ring words [m*K, m*K+K) plus
+// the word just before them, which is exactly the bit range of reference lanes
+// 4m..4m+3, i.e. all 16 k-rows of output columns m and m+8. A lane therefore finishes
+// whole dot products over the tile's 16 k values and needs no cross-lane reduction
+// inside a tile.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+namespace exl3d {
+
+constexpr float kHadScale = 1.0f / 11.313708498984761f;  // 1/sqrt(128), f32
+
+template <typename T, typename U>
+__device__ __forceinline__ T bitcast(U u) {
+  static_assert(sizeof(T) == sizeof(U), "bitcast size");
+  return __builtin_bit_cast(T, u);
+}
+
+// Materialises an f32 value in a register. Every f32 -> f16 conversion goes through it:
+// the backend otherwise folds fptrunc(fmul) (and fptrunc(fadd)) into v_fma_mixlo_f16,
+// which rounds the exact result once, straight to f16, where the reference rounds to
+// f32 first and then to f16.
+__device__ __forceinline__ float f32_rounded(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ f16 to_f16(float v) { return (f16)f32_rounded(v); }
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)bitcast<f16>(h); }
+__device__ __forceinline__ uint16_t f32_to_f16(float v) { return bitcast<uint16_t>(to_f16(v)); }
+
+// ---------------------------------------------------------------------------------
+// Procedural codebooks (reference exl3.cpp:21-42; GPU form trellis_gemm.cpp:333-356).
+// Every intermediate is exact, so the single f16 rounding of the hardware op is the
+// reference's rounding: mcg/3inst add two f16 halves, mul1 is one f16 fma.
+// ---------------------------------------------------------------------------------
+template <int CB>
+__device__ __forceinline__ uint32_t cb_hash(uint32_t s) {
+  if constexpr (CB == 1) return s * 0xCBAC1FEDu;
+  else return s * 89226354u + 64248484u;
+}
+
+template <int CB>
+__device__ __forceinline__ f16 decode_one(uint32_t s) {
+  if constexpr (CB == 2) {
+    const uint32_t h = s * 0x83DCD12Du;
+    const uint32_t sum = __builtin_amdgcn_sad_u8(h, 0u, 0x6400u);  // 0x6400 + byte sum
+    const f16 v = bitcast<f16>((uint16_t)sum);
+    return __builtin_fmaf16(v, bitcast<f16>((uint16_t)0x1EEE), bitcast<f16>((uint16_t)0xC931));
+  } else {
+    const uint32_t m = (cb_hash<CB>(s) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    const f16x2 v = bitcast<f16x2>(m);
+    return v.x + v.y;
+  }
+}
+
+// Two states -> packed (w0, w1), ready for v_dot2_f32_f16.
+template <int CB>
+__device__ __forceinline__ f16x2 decode_pair(uint32_t s0, uint32_t s1) {
+  if constexpr (CB == 2) {
+    const uint32_t a0 = __builtin_amdgcn_sad_u8(s0 * 0x83DCD12Du, 0u, 0x6400u);
+    const uint32_t a1 = __builtin_amdgcn_sad_u8(s1 * 0x83DCD12Du, 0u, 0x6400u);
+    const f16x2 v = bitcast<f16x2>(a0 | (a1 << 16));
+    const f16x2 inv = {bitcast<f16>((uint16_t)0x1EEE), bitcast<f16>((uint16_t)0x1EEE)};
+    const f16x2 bias = {bitcast<f16>((uint16_t)0xC931), bitcast<f16>((uint16_t)0xC931)};
+    return __builtin_elementwise_fma(v, inv, bias);
+  } else {
+    const uint32_t m0 = (cb_hash<CB>(s0) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    const uint32_t m1 = (cb_hash<CB>(s1) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    const uint32_t lo = __builtin_amdgcn_perm(m1, m0, 0x05040100u);  // (m0.lo, m1.lo)
+    const uint32_t hi = __builtin_amdgcn_perm(m1, m0, 0x07060302u);  // (m0.hi, m1.hi)
+    return bitcast<f16x2>(lo) + bitcast<f16x2>(hi);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Ring windows inside one lane's bit string. W[0] is the word before the lane's own
+// words, W[1..K] are its own K words (ring words m*K .. m*K+K-1 of the tile). The lane
+// decodes tile positions p = 32*m + t, t = 0..31, whose windows end at local bit
+// 32 + (t+1)*K; the state's least significant bit is local bit 31 + (t+1)*K.
+// F[w] = the 32 bits straddling W[w-1] | W[w] (low half of W[w-1], high half of W[w]).
+// ---------------------------------------------------------------------------------
+template <int K, int T>
+__device__ __forceinline__ uint32_t lane_state(const uint32_t (&W)[K + 1],
+                                               const uint32_t (&F)[K + 1]) {
+  constexpr int lsb = 31 + (T + 1) * K;
+  constexpr int wi = lsb / 32;
+  constexpr int sh = 31 - (lsb % 32);
+  if constexpr (sh <= 16) return __builtin_amdgcn_ubfe(W[wi], sh, 16);
+  else return __builtin_amdgcn_ubfe(F[wi], sh - 16, 16);
+}
+
+template <int K>
+__device__ __forceinline__ void lane_funnels(const uint32_t (&W)[K + 1], uint32_t (&F)[K + 1]) {
+  F[0] = 0;
+#pragma unroll
+  for (int w = 1; w <= K; ++w) F[w] = __builtin_amdgcn_alignbit(W[w - 1], W[w], 16);
+}
+
+// Loads this lane's K words and the preceding ring word of its tile. `tile` is the
+// tile's first word, m the lane's index inside the tile's 8 lanes.
+template <int K>
+__device__ __forceinline__ void lane_load(const uint32_t *__restrict__ tile, int m,
+                                          uint32_t (&W)[K + 1]) {
+  const uint32_t *p = tile + m * K;
+#pragma unroll
+  for (int w = 0; w < K; ++w) W[w + 1] = __builtin_nontemporal_load(p + w);
+  W[0] = __builtin_nontemporal_load(tile + ((m * K + 8 * K - 1) % (8 * K)));
+}
+
+// The 32 weights of one lane of one tile, multiplied into MB rows of x.
+// X[r] points at the tile's 16 x values of row r as 8 packed f16 pairs (k = 2u, 2u+1).
+// acc[r][0] accumulates output column m, acc[r][1] column m + 8 (m = lane's slot).
+// Position t = 8j + 4h + q covers k-row 2j + {0,1,8,9}[q] of column m + 8h, so
+// (q = 0,1) pairs with x pair j and (q = 2,3) with x pair 4 + j.
+template <int K, int CB, int MB>
+__device__ __forceinline__ void lane_tile_fma(const uint32_t (&W)[K + 1],
+                                              const uint32_t (&X)[MB][8],
+                                              float (&acc)[MB][2]) {
+  uint32_t F[K + 1];
+  lane_funnels<K>(W, F);
+#define EXL3_TILE_STEP(J, H)                                                             \
+  {                                                                                      \
+    const f16x2 wa = decode_pair<CB>(lane_state<K, 8 * J + 4 * H + 0>(W, F),           \
+                                     lane_state<K, 8 * J + 4 * H + 1>(W, F));           \
+    const f16x2 wb = decode_pair<CB>(lane_state<K, 8 * J + 4 * H + 2>(W, F),           \
+                                     lane_state<K, 8 * J + 4 * H + 3>(W, F));           \
+    _Pragma("unroll") for (int r = 0; r < MB; ++r) {                                     \
+      acc[r][H] = __builtin_amdgcn_fdot2(wa, bitcast<f16x2>(X[r][J]), acc[r][H], false); \
+      acc[r][H] = __builtin_amdgcn_fdot2(wb, bitcast<f16x2>(X[r][4 + J]), acc[r][H], false); \
+    }                                                                                    \
+  }
+  EXL3_TILE_STEP(0, 0) EXL3_TILE_STEP(0, 1)
+  EXL3_TILE_STEP(1, 0) EXL3_TILE_STEP(1, 1)
+  EXL3_TILE_STEP(2, 0) EXL3_TILE_STEP(2, 1)
+  EXL3_TILE_STEP(3, 0) EXL3_TILE_STEP(3, 1)
+#undef EXL3_TILE_STEP
+}
+
+// ---------------------------------------------------------------------------------
+// 128-point Sylvester Hadamard over one wave: lane l holds elements 2l and 2l+1.
+// Stage order len = 1, 2, ..., 64 with (x[j], x[j+len]) -> (a + b, a - b), the f32
+// association of reference exl3.cpp:140-150 and trellis_gemm.cpp:387-396.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ void wave_fwht128(float &v0, float &v1) {
+  const int lane = threadIdx.x & 63;
+  {
+    const float a = v0, b = v1;
+    v0 = a + b;
+    v1 = a - b;
+  }
+#pragma unroll
+  for (int s = 0; s < 6; ++s) {
+    const int d = 1 << s;  // lane distance for element distance 2d
+    const float p0 = __shfl_xor(v0, d, 64);
+    const float p1 = __shfl_xor(v1, d, 64);
+    const bool upper = (lane & d) != 0;
+    v0 = upper ? (p0 - v0) : (v0 + p0);
+    v1 = upper ? (p1 - v1) : (v1 + p1);
+  }
+}
+
+// Round-trip helpers for the two sides of a trellis linear (trellis_gemm.cpp:383-399).
+// pre : xhat = f16( fwht(f32(x) * f32(s)) * scale )
+// post: y    = f16( (fwht(f32(f16(yhat))) * scale) * f32(s) )
+__device__ __forceinline__ void wave_had_pre(float &v0, float &v1, float s0, float s1) {
+  v0 = v0 * s0;
+  v1 = v1 * s1;
+  wave_fwht128(v0, v1);
+  v0 = f32_rounded(v0 * kHadScale);
+  v1 = f32_rounded(v1 * kHadScale);
+}
+
+__device__ __forceinline__ void wave_had_post(float &v0, float &v1, float s0, float s1) {
+  v0 = (float)to_f16(v0);
+  v1 = (float)to_f16(v1);
+  wave_fwht128(v0, v1);
+  v0 = f32_rounded(f32_rounded(v0 * kHadScale) * s0);
+  v1 = f32_rounded(f32_rounded(v1 * kHadScale) * s1);
+}
+
+}  // namespace exl3d

@@ -1,0 +1,89 @@
+// Host-side internals shared by the library's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "exl3_moe.h"
+
+namespace exl3h {
+
+// Thread-local last error (exl3_last_error).
+void set_error(const std::string &msg);
+exl3_status fail(exl3_status st, const std::string &msg);
+exl3_status hip_check(hipError_t e, const char *what);
+
+#define EXL3_HIP(call)                                          \
+  do {                                                          \
+    hipError_t e_ = (call);                                     \
+    if (e_ != hipSuccess) return exl3h::hip_check(e_, #call);   \
+  } while (0)
+
+#define EXL3_LAUNCHED(what)                                     \
+  do {                                                          \
+    hipError_t e_ = hipGetLastError();                          \
+    if (e_ != hipSuccess) return exl3h::hip_check(e_, what);    \
+  } while (0)
+
+inline hipStream_t stream_of(exl3_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// The k partition of a trellis GEMV, a function of the tensor shape only (so every
+// entry point that sees a shape sums it in the same f32 order):
+//   waves per workgroup  kWaves (fixed)
+//   k-tiles per wave     T
+//   k-splits             S = k_tiles / (kWaves * T), summed in split order
+// Each output element is ((w0 + w1) + w2) + w3 over the workgroup's waves, then
+// s0 + s1 + ... over splits; inside a wave the k-tiles are visited in order.
+constexpr int kWaves = 4;
+
+struct KPart {
+  int T;
+  int S;
+};
+
+inline KPart kpart(int k_tiles) {
+  int T;
+  if (k_tiles >= 256 && k_tiles % 64 == 0) T = 16;
+  else if (k_tiles % 32 == 0) T = 8;
+  else if (k_tiles % 16 == 0) T = 4;
+  else T = 2;
+  return KPart{T, k_tiles / (kWaves * T)};
+}
+
+// Scheduling knobs (exl3_set_tuning).
+exl3_tuning tuning();
+
+// Validates a trellis descriptor for the Hadamard-based paths.
+exl3_status check_desc(const exl3_trellis_desc *w, bool need_128);
+
+// A small table of per-member device pointers passed by value in kernel arguments.
+struct PtrTable {
+  static constexpr int kMax = 128;
+  const void *p[kMax];
+};
+
+// Launchers implemented in trellis_kernels.hip, used by the API layer.
+exl3_status launch_decode(const exl3_trellis_desc &w, uint16_t *w_hat, hipStream_t st);
+exl3_status launch_reconstruct(const exl3_trellis_desc &w, uint16_t *w_out, hipStream_t st);
+// pre (x16) or post (x32) Hadamard over (rows, n); row r uses scale vector
+// s.p[r / rows_per_member] (rows_per_member = rows when one vector is shared).
+exl3_status launch_hadamard(const uint16_t *x16, const float *x32, int64_t rows, int n,
+                            const PtrTable &s, int64_t rows_per_member, uint16_t *y,
+                            hipStream_t st);
+
+// xhat: (n, rows, in) f16 (member stride rows*in, or 0 when shared); part: f32
+// (n, S, rows, out).
+exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, int n,
+                       const uint16_t *xhat, int64_t x_member_stride, int64_t rows, float *part,
+                       hipStream_t st);
+// Sums the S partials in split order into y32 (raw f32, (n, rows, out)) or, through
+// the output Hadamard with member m's svh.p[m], into y16 (n, rows, out).
+exl3_status launch_qmv_finalize(int n, int S, int64_t rows, int out, const float *part,
+                                float *y32, uint16_t *y16, const PtrTable &svh,
+                                hipStream_t st);
+
+}  // namespace exl3h

@@ -1,0 +1,871 @@
+// MoE layer: router logits, top-k routing + expert-order dispatch (one workgroup, no
+// host round trip), the dense f16 shared expert, and the C ABI of the layer.
+// Reference: src/glm5_moe.{h,cpp} (muyouming/exl3-server).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "exl3_device.hpp"
+#include "exl3_internal.hpp"
+#include "exl3_moe.h"
+#include "moe_common.hpp"
+
+using namespace exl3d;
+using exl3m::ExpertTab;
+using exl3m::MoeArgs;
+
+namespace exl3h {
+exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const MoeArgs &a,
+                              int shared_mode, hipStream_t st);
+}
+
+namespace {
+
+__device__ __forceinline__ float lo16(uint32_t v) { return (float)bitcast<f16>((uint16_t)(v & 0xffffu)); }
+__device__ __forceinline__ float hi16(uint32_t v) { return (float)bitcast<f16>((uint16_t)(v >> 16)); }
+__device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
+
+// ---------------------------------------------------------------------------------
+// Router logits: logits[t][e] = sum_k f32(h[t][k]) * f32(router_w[e][k])
+// (glm5_moe.cpp:127-128). One wave per expert, 8 token rows per workgroup; f16*f16
+// products are exact in f32. Also clears the layer's completion counters.
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_moe_logits(MoeArgs a) {
+  const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+  for (int i = lin * 256 + threadIdx.x; i < a.n_counters; i += gridDim.x * gridDim.y * 256) {
+    if (i < a.n_counters) a.gu_cnt[i] = 0;  // gu_cnt, dn_cnt, comb_cnt are contiguous
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + wave;
+  if (e >= a.E) return;
+  const int r0 = blockIdx.y * 8;
+  const int nr = min(8, a.N - r0);
+  float acc[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+  const uint16_t *wrow = a.router_w + (int64_t)e * a.H;
+  for (int k = lane * 8; k < a.H; k += 512) {
+    const uint4 w4 = *reinterpret_cast<const uint4 *>(wrow + k);
+    const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      if (r >= nr) break;
+      const uint4 x4 = *reinterpret_cast<const uint4 *>(a.h + (int64_t)(r0 + r) * a.H + k);
+      const uint32_t xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[r] = fmaf(lo16(xv[q]), lo16(wv[q]), acc[r]);
+        acc[r] = fmaf(hi16(xv[q]), hi16(wv[q]), acc[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    float v = acc[r];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    if (lane == 0 && r < nr) a.logits[(int64_t)(r0 + r) * a.E + e] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Routing + dispatch, one workgroup of 16 waves (glm5_moe.cpp:16-60, 158-255).
+// ---------------------------------------------------------------------------------
+constexpr int kMaxE = 1024;
+constexpr int kJ = kMaxE / 64;
+
+__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+__device__ __forceinline__ uint64_t match_mask(int e, bool valid) {
+  uint64_t m = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 10; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t bb = __ballot(bit);
+    m &= bit ? bb : ~bb;
+  }
+  return m;
+}
+
+__device__ __forceinline__ uint64_t lanes_below() {
+  const int lane = threadIdx.x & 63;
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+__global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int32_t *id_out,
+                                                    int do_dispatch) {
+  __shared__ float s_buf[16][kMaxE];  // group path: scores_for_choice per wave; dispatch: counts
+  __shared__ int s_keep[16][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int E = a.E, K = a.topk;
+  const int ng = a.n_group > 1 ? a.n_group : 1;
+  const int tg = a.topk_group > 0 ? min(a.topk_group, ng) : 1;
+  const int gsize = E / ng;
+
+  for (int b = wave; b < a.N; b += 16) {
+    float sc[kJ], sfc[kJ];
+    const float *lg = a.logits + (int64_t)b * E;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int e = lane + 64 * j;
+      sc[j] = 0.0f;
+      sfc[j] = -INFINITY;
+      if (e < E) {
+        sc[j] = 1.0f / (1.0f + expf(-lg[e]));
+        sfc[j] = sc[j] + a.router_bias[e];
+      }
+    }
+    if (ng > 1) {
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) s_buf[wave][e] = sfc[j];
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      float gs = -INFINITY;
+      if (lane < ng) {
+        float m1 = -INFINITY, m2 = -INFINITY;
+        for (int j = 0; j < gsize; ++j) {
+          const float v = s_buf[wave][lane * gsize + j];
+          if (v > m1) {
+            m2 = m1;
+            m1 = v;
+          } else if (v > m2) {
+            m2 = v;
+          }
+        }
+        gs = gsize >= 2 ? m1 + m2 : m1;
+      }
+      bool kept = false;
+      for (int i = 0; i < tg; ++i) {
+        float bv = (lane < ng && !kept) ? gs : -INFINITY;
+        int bi = (lane < ng && !kept) ? lane : 1 << 30;
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+          const float ov = __shfl_xor(bv, d, 64);
+          const int oi = __shfl_xor(bi, d, 64);
+          if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+          }
+        }
+        if (lane == bi) kept = true;
+      }
+      s_keep[wave][lane] = kept ? 1 : 0;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E && !s_keep[wave][e / gsize]) sfc[j] = -INFINITY;
+      }
+    }
+    uint32_t taken = 0;
+    float denom = 0.0f;
+    float my_w = 0.0f;
+    int my_id = 0;
+    for (int k = 0; k < K; ++k) {
+      float bv = -INFINITY;
+      int bi = 1 << 30;
+      float bs = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E && !((taken >> j) & 1u) && better(sfc[j], e, bv, bi)) {
+          bv = sfc[j];
+          bi = e;
+          bs = sc[j];
+        }
+      }
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) {
+        const float ov = __shfl_xor(bv, d, 64);
+        const int oi = __shfl_xor(bi, d, 64);
+        const float os = __shfl_xor(bs, d, 64);
+        if (better(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+          bs = os;
+        }
+      }
+      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+      denom += bs;
+      if (lane == k) {
+        my_w = bs;
+        my_id = bi;
+      }
+    }
+    if (lane < K) {
+      float w = my_w;
+      if (a.norm_topk_prob) w = w / (denom + 1e-20f);
+      w = w * a.routed_scaling_factor;
+      w_out[(int64_t)b * K + lane] = w;
+      id_out[(int64_t)b * K + lane] = my_id;
+    }
+  }
+  if (!do_dispatch) return;
+  __syncthreads();
+
+  // Stable counting sort of the P = N*K pairs by expert (pair order b*K + k), the
+  // order of the reference's stable_sort (glm5_moe.cpp:191-200).
+  int *cnt = reinterpret_cast<int *>(&s_buf[0][0]);  // [16][kMaxE]
+  for (int i = threadIdx.x; i < 16 * kMaxE; i += 1024) cnt[i] = 0;
+  __syncthreads();
+  const int P = a.P;
+  const int seg = ((P + 15) / 16 + 63) / 64 * 64;
+  const int pbeg = wave * seg, pend = min(P, pbeg + seg);
+  for (int c = pbeg; c < pend; c += 64) {
+    const int p = c + lane;
+    const bool valid = p < pend;
+    const int e = valid ? id_out[p] : 0;
+    const uint64_t m = match_mask(e, valid);
+    if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // Per expert: total, base offset (exclusive scan over experts), per-wave offsets.
+  const int t = threadIdx.x;
+  int tot = 0;
+  if (t < E)
+    for (int w = 0; w < 16; ++w) tot += cnt[w * kMaxE + t];
+  // block exclusive scan of tot and of (tot > 0)
+  int v = tot, f = tot > 0 ? 1 : 0;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int ov = __shfl_up(v, d, 64), of = __shfl_up(f, d, 64);
+    if (lane >= d) {
+      v += ov;
+      f += of;
+    }
+  }
+  __shared__ int s_wv[16], s_wf[16];
+  if (lane == 63) {
+    s_wv[wave] = v;
+    s_wf[wave] = f;
+  }
+  __syncthreads();
+  int pv = 0, pf = 0;
+  for (int w = 0; w < wave; ++w) {
+    pv += s_wv[w];
+    pf += s_wf[w];
+  }
+  const int base_e = pv + v - tot;           // exclusive
+  const int run_i = pf + f - (tot > 0 ? 1 : 0);
+  if (t < E) {
+    int run = base_e;
+    for (int w = 0; w < 16; ++w) {
+      const int x = cnt[w * kMaxE + t];
+      cnt[w * kMaxE + t] = run;
+      run += x;
+    }
+    if (tot > 0) {
+      a.run_expert[run_i] = t;
+      a.run_off[run_i] = base_e;
+      a.run_len[run_i] = tot;
+    }
+  }
+  if (t == 1023) {
+    int nrun = 0;
+    for (int w = 0; w < 16; ++w) nrun += s_wf[w];
+    *a.n_runs = nrun;
+  }
+  __syncthreads();
+  for (int c = pbeg; c < pend; c += 64) {
+    const int p = c + lane;
+    const bool valid = p < pend;
+    const int e = valid ? id_out[p] : 0;
+    const uint64_t m = match_mask(e, valid);
+    if (valid) {
+      const int pos = cnt[wave * kMaxE + e] + __builtin_popcountll(m & lanes_below());
+      a.sorted_row[pos] = p / K;
+      a.sorted_rank[pos] = p % K;
+      a.slot[p] = pos;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
+    __builtin_amdgcn_wave_barrier();
+  }
+  for (int i = threadIdx.x; i < a.N; i += 1024) {
+    a.sorted_row[P + i] = i;
+    a.sorted_rank[P + i] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Dense f16 shared expert (g5_linear's mx::matmul branch, glm5_kda.cpp:120):
+// part[s][row][n] = sum over k in [128 s, 128 s + 128) of x[row][k] * W[k][n].
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_dense_part(const uint16_t *__restrict__ x, int64_t rows,
+                                                    int in, int out,
+                                                    const uint16_t *__restrict__ W,
+                                                    float *__restrict__ part) {
+  __shared__ uint32_t xs[16][64];
+  const int n = blockIdx.x * 512 + 2 * threadIdx.x;
+  const int s = blockIdx.y, k0 = s * 128;
+  for (int64_t r0 = 0; r0 < rows; r0 += 16) {
+    const int nr = (int)min<int64_t>(16, rows - r0);
+    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+      const int r = i >> 6, wd = i & 63;
+      xs[r][wd] = r < nr ? reinterpret_cast<const uint32_t *>(x + (r0 + r) * in + k0)[wd] : 0u;
+    }
+    __syncthreads();
+    float acc[16][2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r][0] = acc[r][1] = 0.0f;
+    if (n < out) {
+      for (int k = 0; k < 128; k += 2) {
+        const uint32_t w0 = *reinterpret_cast<const uint32_t *>(W + (int64_t)(k0 + k) * out + n);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t *>(W + (int64_t)(k0 + k + 1) * out + n);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t xv = xs[r][k >> 1];
+          acc[r][0] = fmaf(lo16(xv), lo16(w0), acc[r][0]);
+          acc[r][1] = fmaf(lo16(xv), hi16(w0), acc[r][1]);
+          acc[r][0] = fmaf(hi16(xv), lo16(w1), acc[r][0]);
+          acc[r][1] = fmaf(hi16(xv), hi16(w1), acc[r][1]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (r >= nr) break;
+        float *p = part + ((int64_t)s * rows + r0 + r) * out + n;
+        p[0] = acc[r][0];
+        p[1] = acc[r][1];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ float swiglu1(float g, float u, float L) {
+  if (L > 0.0f) {
+    g = fminf(g, L);
+    u = fminf(fmaxf(u, -L), L);
+  }
+  const float sg = rf16(1.0f / (1.0f + expf(-g)));
+  const float act = rf16(g * sg);
+  return rf16(act * u);
+}
+
+// act[row][c] = swiglu(f16(sum_s gate part), f16(sum_s up part))
+__global__ __launch_bounds__(256) void k_dense_swiglu(const float *__restrict__ pg,
+                                                      const float *__restrict__ pu, int S,
+                                                      int64_t rows, int n, float limit,
+                                                      uint16_t *__restrict__ act) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * n) return;
+  float g = pg[i], u = pu[i];
+  for (int s = 1; s < S; ++s) {
+    g += pg[(int64_t)s * rows * n + i];
+    u += pu[(int64_t)s * rows * n + i];
+  }
+  const float L = limit > 0.0f ? rf16(limit) : 0.0f;
+  act[i] = bitcast<uint16_t>(to_f16(swiglu1(rf16(g), rf16(u), L)));
+}
+
+__global__ __launch_bounds__(256) void k_dense_out(const float *__restrict__ p, int S, int64_t count,
+                                                   uint16_t *__restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  float v = p[i];
+  for (int s = 1; s < S; ++s) v += p[(int64_t)s * count + i];
+  y[i] = bitcast<uint16_t>(to_f16(v));
+}
+
+}  // namespace
+
+using namespace exl3h;
+
+// ---------------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------------
+struct exl3_moe_layer_s {
+  exl3_moe_config cfg;
+  int H, I, E, topk;
+  int gu_K, gu_cb, dn_K, dn_cb;
+  int shared;        // 0 none, 1 trellis, 2 dense
+  int SI, sh_K, sh_cb, sh_dn_K, sh_dn_cb;
+  const uint16_t *sh_dense[3];
+  const uint16_t *router_w;
+  const float *router_bias;
+  ExpertTab *tab_dev;  // E + 1 entries
+  std::vector<int64_t> expert_bytes;  // trellis bytes (+ scales) per routed expert
+  std::vector<int64_t> gu_bytes, dn_bytes;  // trellis bytes of gate+up / down per expert
+  int diag_on;
+  exl3_moe_diag diag;
+  int timing_on;
+  exl3_moe_timing timing;
+  hipEvent_t ev[5];
+  bool ev_made;
+  std::mutex mu;
+};
+
+namespace {
+
+struct MoeLayout {
+  size_t total;
+  size_t logits, weights, ids, sorted_row, sorted_rank, slot, run_expert, run_off, run_len, n_runs;
+  size_t gu_part, act_hat, dn_part, yw, sh_out, counters, dsh_part, dsh_act;
+  int P, R, Imax, Sgu, Sdn, cnt_stride, n_counters;
+  int64_t dsh_part_elems;
+};
+
+MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
+  MoeLayout m{};
+  const int H = L->H, I = L->I, E = L->E, K = L->topk, SI = L->shared ? L->SI : 0;
+  m.P = (int)(N * K);
+  m.R = std::min<int64_t>(E, m.P);
+  m.Imax = std::max(I, SI);
+  m.Sgu = kpart(H / 16).S;
+  m.Sdn = std::max(kpart(I / 16).S, SI ? kpart(SI / 16).S : 1);
+  m.cnt_stride = std::max(m.Imax / 128, H / 128);
+  m.n_counters = (int)(2 * (int64_t)(m.R + 1) * m.cnt_stride + N * (H / 128));
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align_up(o + bytes, 256);
+    return at;
+  };
+  const int64_t slots = m.P + N;
+  m.logits = take(4 * N * E);
+  m.weights = take(4 * (size_t)m.P);
+  m.ids = take(4 * (size_t)m.P);
+  m.sorted_row = take(4 * (size_t)slots);
+  m.sorted_rank = take(4 * (size_t)slots);
+  m.slot = take(4 * (size_t)m.P);
+  m.run_expert = take(4 * (size_t)m.R);
+  m.run_off = take(4 * (size_t)m.R);
+  m.run_len = take(4 * (size_t)m.R);
+  m.n_runs = take(4);
+  m.gu_part = take(4 * (size_t)slots * 2 * m.Sgu * m.Imax);
+  m.act_hat = take(2 * (size_t)slots * m.Imax);
+  m.dn_part = take(4 * (size_t)slots * m.Sdn * H);
+  m.yw = take(2 * (size_t)m.P * H);
+  m.sh_out = take(2 * (size_t)N * H);
+  m.counters = take(4 * (size_t)m.n_counters);
+  m.dsh_part_elems = 0;
+  if (L->shared == 2) {
+    m.dsh_part_elems = std::max<int64_t>(2 * (int64_t)(H / 128) * N * SI, (int64_t)(SI / 128) * N * H);
+  }
+  m.dsh_part = take(4 * (size_t)m.dsh_part_elems);
+  m.dsh_act = take(2 * (size_t)N * (L->shared == 2 ? SI : 0));
+  m.total = o;
+  return m;
+}
+
+MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, const uint16_t *h,
+                  uint16_t *out, char *ws) {
+  MoeArgs a{};
+  a.N = (int)N;
+  a.H = L->H;
+  a.I = L->I;
+  a.SI = L->shared ? L->SI : 0;
+  a.Imax = m.Imax;
+  a.E = L->E;
+  a.topk = L->topk;
+  a.P = m.P;
+  a.R = m.R;
+  a.n_group = L->cfg.n_group;
+  a.topk_group = L->cfg.topk_group;
+  a.norm_topk_prob = L->cfg.norm_topk_prob;
+  a.routed_scaling_factor = L->cfg.routed_scaling_factor;
+  a.swiglu_limit = L->cfg.swiglu_limit;
+  a.has_shared = L->shared ? 1 : 0;
+  a.Sgu = m.Sgu;
+  a.Sdn = m.Sdn;
+  a.cnt_stride = m.cnt_stride;
+  a.h = h;
+  a.router_w = L->router_w;
+  a.router_bias = L->router_bias;
+  a.tab = L->tab_dev;
+  a.logits = (float *)(ws + m.logits);
+  a.weights = (float *)(ws + m.weights);
+  a.ids = (int32_t *)(ws + m.ids);
+  a.sorted_row = (int32_t *)(ws + m.sorted_row);
+  a.sorted_rank = (int32_t *)(ws + m.sorted_rank);
+  a.slot = (int32_t *)(ws + m.slot);
+  a.run_expert = (int32_t *)(ws + m.run_expert);
+  a.run_off = (int32_t *)(ws + m.run_off);
+  a.run_len = (int32_t *)(ws + m.run_len);
+  a.n_runs = (int32_t *)(ws + m.n_runs);
+  a.gu_part = (float *)(ws + m.gu_part);
+  a.act_hat = (uint16_t *)(ws + m.act_hat);
+  a.dn_part = (float *)(ws + m.dn_part);
+  a.yw = (uint16_t *)(ws + m.yw);
+  a.sh_out = (uint16_t *)(ws + m.sh_out);
+  a.gu_cnt = (uint32_t *)(ws + m.counters);
+  a.dn_cnt = a.gu_cnt + (int64_t)(m.R + 1) * m.cnt_stride;
+  a.comb_cnt = a.dn_cnt + (int64_t)(m.R + 1) * m.cnt_stride;
+  a.n_counters = m.n_counters;
+  a.dsh_part = (float *)(ws + m.dsh_part);
+  a.dsh_act = (uint16_t *)(ws + m.dsh_act);
+  a.out = out;
+  return a;
+}
+
+exl3_status check_linear(const exl3_linear_desc &d, int in, int out, const char *what) {
+  if (d.in_features != in || d.out_features != out)
+    return fail(EXL3_ERR_INVALID, std::string(what) + ": shape mismatch");
+  if (d.dense) return EXL3_OK;
+  exl3_status rc = check_desc(&d.tw, true);
+  if (rc) return fail(rc, std::string(what) + ": " + exl3_last_error());
+  if (d.tw.in_features != in || d.tw.out_features != out)
+    return fail(EXL3_ERR_INVALID, std::string(what) + ": trellis shape mismatch");
+  return EXL3_OK;
+}
+
+exl3_status launch_logits_route(exl3_moe_layer_s *L, const MoeArgs &a, float *w_out, int32_t *id_out,
+                                int do_dispatch, hipStream_t st) {
+  dim3 g1((unsigned)((a.E + 3) / 4), (unsigned)((a.N + 7) / 8));
+  k_moe_logits<<<g1, 256, 0, st>>>(a);
+  EXL3_LAUNCHED("k_moe_logits");
+  k_moe_route<<<1, 1024, 0, st>>>(a, w_out, id_out, do_dispatch);
+  EXL3_LAUNCHED("k_moe_route");
+  (void)L;
+  return EXL3_OK;
+}
+
+exl3_status check_ws(void *ws, size_t bytes, size_t need) {
+  if (!ws || bytes < need)
+    return fail(EXL3_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
+                                        " bytes, got " + std::to_string(bytes));
+  if (reinterpret_cast<uintptr_t>(ws) % 256)
+    return fail(EXL3_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return EXL3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_moe_config *cfg,
+                                  exl3_moe_layer_t *out) {
+  if (!desc || !cfg || !out) return fail(EXL3_ERR_INVALID, "null argument");
+  *out = nullptr;
+  const int H = cfg->hidden_size, I = cfg->moe_intermediate_size, E = cfg->n_routed_experts;
+  const int K = cfg->num_experts_per_tok;
+  if (H <= 0 || H % 128 || I <= 0 || I % 128)
+    return fail(EXL3_ERR_INVALID, "hidden and intermediate sizes must be positive multiples of 128");
+  if (E <= 0 || E > 1024) return fail(EXL3_ERR_UNSUPPORTED, "n_routed_experts must be in 1..1024");
+  if (K <= 0 || K > E || K > 64) return fail(EXL3_ERR_INVALID, "num_experts_per_tok must be in 1..min(E, 64)");
+  const int ng = cfg->n_group > 1 ? cfg->n_group : 1;
+  if (ng > 64 || E % ng) return fail(EXL3_ERR_INVALID, "n_group must divide E and be <= 64");
+  if (!desc->experts || !desc->router_w || !desc->router_bias)
+    return fail(EXL3_ERR_INVALID, "missing experts or router tensors");
+  const exl3_linear_desc *ex = desc->experts;
+  for (int e = 0; e < E; ++e) {
+    for (int j = 0; j < 3; ++j) {
+      const exl3_linear_desc &d = ex[3 * e + j];
+      exl3_status rc = check_linear(d, j == 2 ? I : H, j == 2 ? H : I, "expert");
+      if (rc) return rc;
+      if (d.dense) return fail(EXL3_ERR_UNSUPPORTED, "routed experts must be EXL3 trellis tensors");
+      const exl3_linear_desc &r0 = ex[j == 2 ? 2 : 0];
+      if (d.tw.K != r0.tw.K || d.tw.codebook != r0.tw.codebook)
+        return fail(EXL3_ERR_INVALID,
+                    "every routed gate/up (and every down) projection must share K and codebook");
+    }
+  }
+  auto *L = new exl3_moe_layer_s();
+  L->cfg = *cfg;
+  L->H = H;
+  L->I = I;
+  L->E = E;
+  L->topk = K;
+  L->gu_K = ex[0].tw.K;
+  L->gu_cb = ex[0].tw.codebook;
+  L->dn_K = ex[2].tw.K;
+  L->dn_cb = ex[2].tw.codebook;
+  L->router_w = desc->router_w;
+  L->router_bias = desc->router_bias;
+  L->shared = 0;
+  L->SI = 0;
+  if (desc->shared) {
+    const exl3_linear_desc *sh = desc->shared;
+    const int SI = sh[0].out_features;
+    if (SI <= 0 || SI % 128) {
+      delete L;
+      return fail(EXL3_ERR_INVALID, "shared intermediate must be a positive multiple of 128");
+    }
+    for (int j = 0; j < 3; ++j) {
+      exl3_status rc = check_linear(sh[j], j == 2 ? SI : H, j == 2 ? H : SI, "shared expert");
+      if (rc) {
+        delete L;
+        return rc;
+      }
+    }
+    const bool dense = sh[0].dense && sh[1].dense && sh[2].dense;
+    const bool quant = !sh[0].dense && !sh[1].dense && !sh[2].dense;
+    if (!dense && !quant) {
+      delete L;
+      return fail(EXL3_ERR_UNSUPPORTED, "shared expert must be all-trellis or all-f16");
+    }
+    if (quant && (sh[0].tw.K != sh[1].tw.K || sh[0].tw.codebook != sh[1].tw.codebook)) {
+      delete L;
+      return fail(EXL3_ERR_INVALID, "shared gate/up must share K and codebook");
+    }
+    L->SI = SI;
+    L->shared = dense ? 2 : 1;
+    L->sh_K = quant ? sh[0].tw.K : 0;
+    L->sh_cb = quant ? sh[0].tw.codebook : 0;
+    L->sh_dn_K = quant ? sh[2].tw.K : 0;
+    L->sh_dn_cb = quant ? sh[2].tw.codebook : 0;
+    for (int j = 0; j < 3; ++j) L->sh_dense[j] = sh[j].dense;
+  }
+  std::vector<ExpertTab> tab((size_t)E + 1);
+  L->expert_bytes.resize(E);
+  L->gu_bytes.resize(E);
+  L->dn_bytes.resize(E);
+  for (int e = 0; e < E; ++e) {
+    int64_t bytes[3];
+    for (int j = 0; j < 3; ++j) {
+      const exl3_trellis_desc &t = ex[3 * e + j].tw;
+      tab[e].tr[j] = (const uint32_t *)t.trellis;
+      tab[e].suh[j] = t.suh;
+      tab[e].svh[j] = t.svh;
+      bytes[j] = (int64_t)t.in_features * t.out_features / 256 * 32 * t.K;
+    }
+    L->gu_bytes[e] = bytes[0] + bytes[1];
+    L->dn_bytes[e] = bytes[2];
+    L->expert_bytes[e] = bytes[0] + bytes[1] + bytes[2];
+  }
+  if (L->shared == 1) {
+    for (int j = 0; j < 3; ++j) {
+      const exl3_trellis_desc &t = desc->shared[j].tw;
+      tab[E].tr[j] = (const uint32_t *)t.trellis;
+      tab[E].suh[j] = t.suh;
+      tab[E].svh[j] = t.svh;
+    }
+  }
+  hipError_t e1 = hipMalloc(&L->tab_dev, sizeof(ExpertTab) * tab.size());
+  if (e1 != hipSuccess) {
+    delete L;
+    return hip_check(e1, "hipMalloc(expert table)");
+  }
+  e1 = hipMemcpy(L->tab_dev, tab.data(), sizeof(ExpertTab) * tab.size(), hipMemcpyHostToDevice);
+  if (e1 != hipSuccess) {
+    (void)hipFree(L->tab_dev);
+    delete L;
+    return hip_check(e1, "hipMemcpy(expert table)");
+  }
+  L->diag_on = 0;
+  std::memset(&L->diag, 0, sizeof(L->diag));
+  L->timing_on = 0;
+  std::memset(&L->timing, 0, sizeof(L->timing));
+  L->ev_made = false;
+  *out = L;
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer) {
+  if (!layer) return EXL3_OK;
+  if (layer->ev_made)
+    for (int i = 0; i < 5; ++i) (void)hipEventDestroy(layer->ev[i]);
+  if (layer->tab_dev) {
+    hipError_t e = hipFree(layer->tab_dev);
+    if (e != hipSuccess) {
+      delete layer;
+      return hip_check(e, "hipFree(expert table)");
+    }
+  }
+  delete layer;
+  return EXL3_OK;
+}
+
+size_t exl3_moe_workspace_size(exl3_moe_layer_t layer, int64_t rows) {
+  if (!layer || rows <= 0) return 0;
+  return moe_layout(layer, rows).total;
+}
+
+exl3_status exl3_moe_route(exl3_moe_layer_t layer, const uint16_t *h, int64_t rows, float *weights,
+                           int32_t *ids, void *workspace, size_t workspace_bytes,
+                           exl3_stream_t stream) {
+  if (!layer || !h || !weights || !ids || rows < 0) return fail(EXL3_ERR_INVALID, "bad route arguments");
+  if (rows == 0) return EXL3_OK;
+  const MoeLayout m = moe_layout(layer, rows);
+  exl3_status rc = check_ws(workspace, workspace_bytes, m.total);
+  if (rc) return rc;
+  const MoeArgs a = make_args(layer, m, rows, h, nullptr, (char *)workspace);
+  return launch_logits_route(layer, a, weights, ids, 0, stream_of(stream));
+}
+
+exl3_status exl3_moe_topk_route(const float *logits, const float *bias, int64_t rows,
+                                const exl3_moe_config *cfg, float *weights, int32_t *ids,
+                                exl3_stream_t stream) {
+  if (!logits || !bias || !cfg || !weights || !ids || rows < 0)
+    return fail(EXL3_ERR_INVALID, "bad topk_route arguments");
+  const int E = cfg->n_routed_experts, K = cfg->num_experts_per_tok;
+  const int ng = cfg->n_group > 1 ? cfg->n_group : 1;
+  if (E <= 0 || E > 1024) return fail(EXL3_ERR_UNSUPPORTED, "n_routed_experts must be in 1..1024");
+  if (K <= 0 || K > E || K > 64) return fail(EXL3_ERR_INVALID, "num_experts_per_tok must be in 1..min(E, 64)");
+  if (ng > 64 || E % ng) return fail(EXL3_ERR_INVALID, "n_group must divide E and be <= 64");
+  if (rows == 0) return EXL3_OK;
+  if (rows > (1 << 24)) return fail(EXL3_ERR_UNSUPPORTED, "too many rows");
+  MoeArgs a{};
+  a.N = (int)rows;
+  a.E = E;
+  a.topk = K;
+  a.P = (int)(rows * K);
+  a.n_group = cfg->n_group;
+  a.topk_group = cfg->topk_group;
+  a.norm_topk_prob = cfg->norm_topk_prob;
+  a.routed_scaling_factor = cfg->routed_scaling_factor;
+  a.router_bias = bias;
+  a.logits = const_cast<float *>(logits);
+  k_moe_route<<<1, 1024, 0, stream_of(stream)>>>(a, weights, ids, 0);
+  EXL3_LAUNCHED("k_moe_route");
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B, int64_t Lq,
+                           uint16_t *out, void *workspace, size_t workspace_bytes,
+                           exl3_stream_t stream) {
+  if (!layer || !h || !out || B < 0 || Lq < 0) return fail(EXL3_ERR_INVALID, "bad layer arguments");
+  const int64_t N = B * Lq;
+  if (N == 0) return EXL3_OK;
+  if (N > (1 << 24) / layer->topk) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
+  const MoeLayout m = moe_layout(layer, N);
+  exl3_status rc = check_ws(workspace, workspace_bytes, m.total);
+  if (rc) return rc;
+  hipStream_t st = stream_of(stream);
+  const MoeArgs a = make_args(layer, m, N, h, out, (char *)workspace);
+  const bool timed = layer->timing_on != 0;
+  if (timed && !layer->ev_made) {
+    for (int i = 0; i < 5; ++i) EXL3_HIP(hipEventCreate(&layer->ev[i]));
+    layer->ev_made = true;
+  }
+  if (timed) EXL3_HIP(hipEventRecord(layer->ev[0], st));
+  rc = launch_logits_route(layer, a, a.weights, a.ids, 1, st);
+  if (rc) return rc;
+  if (timed) EXL3_HIP(hipEventRecord(layer->ev[1], st));
+
+  const int H = layer->H;
+  if (layer->shared == 2) {
+    const int SI = layer->SI;
+    const int S1 = H / 128, S2 = SI / 128;
+    float *pg = a.dsh_part, *pu = a.dsh_part + (int64_t)S1 * N * SI;
+    k_dense_part<<<dim3((SI + 511) / 512, S1), 256, 0, st>>>(h, N, H, SI, layer->sh_dense[0], pg);
+    k_dense_part<<<dim3((SI + 511) / 512, S1), 256, 0, st>>>(h, N, H, SI, layer->sh_dense[1], pu);
+    EXL3_LAUNCHED("k_dense_part");
+    k_dense_swiglu<<<(unsigned)((N * SI + 255) / 256), 256, 0, st>>>(pg, pu, S1, N, SI,
+                                                                     layer->cfg.swiglu_limit, a.dsh_act);
+    EXL3_LAUNCHED("k_dense_swiglu");
+    k_dense_part<<<dim3((H + 511) / 512, S2), 256, 0, st>>>(a.dsh_act, N, SI, H, layer->sh_dense[2],
+                                                            a.dsh_part);
+    EXL3_LAUNCHED("k_dense_part");
+    k_dense_out<<<(unsigned)((N * H + 255) / 256), 256, 0, st>>>(a.dsh_part, S2, N * H, a.sh_out);
+    EXL3_LAUNCHED("k_dense_out");
+  } else if (layer->shared == 1) {
+    const int SI = layer->SI;
+    const unsigned gu_blocks = (unsigned)(2 * (SI / 128) * kpart(H / 16).S);
+    rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, gu_blocks, a, 1, st);
+    if (rc) return rc;
+    const unsigned dn_blocks = (unsigned)((H / 128) * kpart(SI / 16).S);
+    rc = launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, dn_blocks, a, 1, st);
+    if (rc) return rc;
+  }
+  if (timed) EXL3_HIP(hipEventRecord(layer->ev[2], st));
+  const int I = layer->I;
+  const unsigned gu_blocks = (unsigned)((int64_t)m.R * 2 * (I / 128) * kpart(H / 16).S);
+  rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, gu_blocks, a, 0, st);
+  if (rc) return rc;
+  if (timed) EXL3_HIP(hipEventRecord(layer->ev[3], st));
+  const unsigned dn_blocks = (unsigned)((int64_t)m.R * (H / 128) * kpart(I / 16).S);
+  rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb, dn_blocks, a, 0, st);
+  if (rc) return rc;
+  if (timed) {
+    EXL3_HIP(hipEventRecord(layer->ev[4], st));
+    EXL3_HIP(hipEventSynchronize(layer->ev[4]));
+    float ms[4];
+    for (int i = 0; i < 4; ++i) EXL3_HIP(hipEventElapsedTime(&ms[i], layer->ev[i], layer->ev[i + 1]));
+    int32_t nr = 0;
+    EXL3_HIP(hipMemcpy(&nr, a.n_runs, 4, hipMemcpyDeviceToHost));
+    std::vector<int32_t> re(nr);
+    if (nr > 0) EXL3_HIP(hipMemcpy(re.data(), a.run_expert, 4 * (size_t)nr, hipMemcpyDeviceToHost));
+    std::lock_guard<std::mutex> lk(layer->mu);
+    exl3_moe_timing &t = layer->timing;
+    t.calls += 1;
+    t.router_ms += ms[0];
+    t.shared_ms += ms[1];
+    t.gate_up_ms += ms[2];
+    t.down_ms += ms[3];
+    t.total_ms += ms[0] + ms[1] + ms[2] + ms[3];
+    for (int i = 0; i < nr; ++i) {
+      t.gate_up_trellis_bytes += layer->gu_bytes[re[i]];
+      t.down_trellis_bytes += layer->dn_bytes[re[i]];
+    }
+  }
+
+  if (layer->diag_on) {
+    std::lock_guard<std::mutex> lk(layer->mu);
+    EXL3_HIP(hipStreamSynchronize(st));
+    int32_t nr = 0;
+    EXL3_HIP(hipMemcpy(&nr, a.n_runs, 4, hipMemcpyDeviceToHost));
+    std::vector<int32_t> rl(nr), re(nr);
+    if (nr > 0) {
+      EXL3_HIP(hipMemcpy(rl.data(), a.run_len, 4 * (size_t)nr, hipMemcpyDeviceToHost));
+      EXL3_HIP(hipMemcpy(re.data(), a.run_expert, 4 * (size_t)nr, hipMemcpyDeviceToHost));
+    }
+    exl3_moe_diag &d = layer->diag;
+    d.calls += 1;
+    d.pairs += m.P;
+    d.runs += nr;
+    d.distinct_experts += nr;
+    for (int i = 0; i < nr; ++i) {
+      const int r = rl[i];
+      d.run_hist[r >= 64 ? 64 : r] += 1;
+      d.shared_bytes += layer->expert_bytes[re[i]];
+      d.streamed_bytes += layer->expert_bytes[re[i]] * ((r + 3) / 4);
+    }
+  }
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_timing_enable(exl3_moe_layer_t layer, int32_t enabled) {
+  if (!layer) return fail(EXL3_ERR_INVALID, "null layer");
+  layer->timing_on = enabled ? 1 : 0;
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_timing_get(exl3_moe_layer_t layer, exl3_moe_timing *out) {
+  if (!layer || !out) return fail(EXL3_ERR_INVALID, "null argument");
+  std::lock_guard<std::mutex> lk(layer->mu);
+  *out = layer->timing;
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_timing_reset(exl3_moe_layer_t layer) {
+  if (!layer) return fail(EXL3_ERR_INVALID, "null layer");
+  std::lock_guard<std::mutex> lk(layer->mu);
+  std::memset(&layer->timing, 0, sizeof(layer->timing));
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_diag_enable(exl3_moe_layer_t layer, int32_t enabled) {
+  if (!layer) return fail(EXL3_ERR_INVALID, "null layer");
+  layer->diag_on = enabled ? 1 : 0;
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_diag_get(exl3_moe_layer_t layer, exl3_moe_diag *out) {
+  if (!layer || !out) return fail(EXL3_ERR_INVALID, "null argument");
+  std::lock_guard<std::mutex> lk(layer->mu);
+  *out = layer->diag;
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_diag_reset(exl3_moe_layer_t layer) {
+  if (!layer) return fail(EXL3_ERR_INVALID, "null layer");
+  std::lock_guard<std::mutex> lk(layer->mu);
+  std::memset(&layer->diag, 0, sizeof(layer->diag));
+  return EXL3_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,326 @@
+// Trellis tensor kernels for gfx950: decode (W_hat), reconstruct (W), the Hadamard
+// steps, and the dequant-GEMV (QMV) with its split-sum / output-Hadamard epilogue.
+//
+// Reference counterparts (muyouming/exl3-server):
+//   decode       exl3.cpp:101-125      (bit-exact)
+//   reconstruct  exl3.cpp:152-209      (bit-exact: same f32 butterfly order, one RNE)
+//   hadamard     trellis_gemm.cpp:367-400, 582-603 (same rounding points)
+//   qmv          trellis_gemm.cpp:30-141 (Metal scalar QMV) + mx::sum over splits
+//                (:980, :1185) + the output Hadamard (:1186)
+#include <hip/hip_runtime.h>
+
+#include "exl3_device.hpp"
+#include "exl3_internal.hpp"
+#include "qmv_core.hpp"
+
+using namespace exl3d;
+
+namespace {
+
+// ---------------------------------------------------------------------------------
+// decode: one workgroup per tile, one thread per stream position.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ int tile_element(int p) {
+  const int L = p >> 3, i = p & 7, q = i & 3;
+  const int row = 2 * (L & 3) + (q < 2 ? q : q + 6);
+  const int col = (L >> 2) + 8 * (i >> 2);
+  return row * 16 + col;
+}
+
+__device__ __forceinline__ uint32_t tile_state_rt(const uint32_t *__restrict__ tile, int K, int p) {
+  const int nw = 8 * K;
+  const int lb = (p + 1) * K - 1;  // ring bit of the state's LSB
+  const int last = lb >> 5;
+  const uint32_t lo = tile[last % nw];
+  const uint32_t hi = tile[(last - 1 + nw) % nw];
+  const uint64_t pair = ((uint64_t)hi << 32) | lo;
+  return (uint32_t)(pair >> (31 - (lb & 31))) & 0xffffu;
+}
+
+template <int CB>
+__global__ __launch_bounds__(256) void k_decode(const uint32_t *__restrict__ trellis, int K,
+                                                int tiles_n, int out, uint16_t *__restrict__ w_hat) {
+  const int tn = blockIdx.x, tk = blockIdx.y, p = threadIdx.x;
+  const uint32_t *tile = trellis + ((int64_t)tk * tiles_n + tn) * 8 * K;
+  const f16 v = decode_one<CB>(tile_state_rt(tile, K, p));
+  const int e = tile_element(p);
+  w_hat[(int64_t)(tk * 16 + (e >> 4)) * out + tn * 16 + (e & 15)] = bitcast<uint16_t>(v);
+}
+
+// ---------------------------------------------------------------------------------
+// reconstruct: one workgroup per 128x128 block. The block is decoded into LDS as f32,
+// then the left butterflies (across rows), the row scale, the right butterflies
+// (across columns), the column scale and one RNE -- the operation order of
+// exl3.cpp:156-197, element for element.
+// ---------------------------------------------------------------------------------
+template <int CB>
+__global__ __launch_bounds__(256) void k_reconstruct(const uint32_t *__restrict__ trellis, int K,
+                                                     int tiles_n, int out,
+                                                     const uint16_t *__restrict__ suh,
+                                                     const uint16_t *__restrict__ svh,
+                                                     uint16_t *__restrict__ w) {
+  __shared__ float buf[128][129];
+  const int cbk = blockIdx.x, rbk = blockIdx.y, tid = threadIdx.x;
+  for (int idx = tid; idx < 64 * 256; idx += 256) {
+    const int t = idx >> 8, p = idx & 255;
+    const int tr = t >> 3, tc = t & 7;
+    const uint32_t *tile =
+        trellis + ((int64_t)(rbk * 8 + tr) * tiles_n + (cbk * 8 + tc)) * 8 * K;
+    const int e = tile_element(p);
+    buf[tr * 16 + (e >> 4)][tc * 16 + (e & 15)] = (float)decode_one<CB>(tile_state_rt(tile, K, p));
+  }
+  __syncthreads();
+  for (int len = 1; len < 128; len <<= 1) {
+    for (int idx = tid; idx < 64 * 128; idx += 256) {
+      const int q = idx >> 7, c = idx & 127;
+      const int j = (q / len) * 2 * len + (q % len);
+      const float a = buf[j][c], b = buf[j + len][c];
+      buf[j][c] = a + b;
+      buf[j + len][c] = a - b;
+    }
+    __syncthreads();
+  }
+  for (int idx = tid; idx < 128 * 128; idx += 256) {
+    const int i = idx >> 7, c = idx & 127;
+    const float s = f16_to_f32(suh[rbk * 128 + i]) * kHadScale;
+    buf[i][c] = buf[i][c] * s;
+  }
+  __syncthreads();
+  for (int len = 1; len < 128; len <<= 1) {
+    for (int idx = tid; idx < 128 * 64; idx += 256) {
+      const int i = idx >> 6, q = idx & 63;
+      const int j = (q / len) * 2 * len + (q % len);
+      const float a = buf[i][j], b = buf[i][j + len];
+      buf[i][j] = a + b;
+      buf[i][j + len] = a - b;
+    }
+    __syncthreads();
+  }
+  for (int idx = tid; idx < 128 * 128; idx += 256) {
+    const int i = idx >> 7, c = idx & 127;
+    const float s = f16_to_f32(svh[cbk * 128 + c]) * kHadScale;
+    w[(int64_t)(rbk * 128 + i) * out + cbk * 128 + c] = f32_to_f16(buf[i][c] * s);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Hadamard pre/post: one wave per (row, 128-block).
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_hadamard(const uint16_t *__restrict__ x16,
+                                                  const float *__restrict__ x32, int64_t rows,
+                                                  int n, exl3h::PtrTable s,
+                                                  int64_t rows_per_member,
+                                                  uint16_t *__restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nb = n / 128;
+  if (gw >= rows * nb) return;
+  const int blk = (int)(gw % nb);
+  const int64_t row = gw / nb;
+  const uint16_t *sv = (const uint16_t *)s.p[row / rows_per_member] + blk * 128 + 2 * lane;
+  const int64_t o = row * n + blk * 128 + 2 * lane;
+  float v0, v1;
+  if (x16) {
+    v0 = f16_to_f32(x16[o]);
+    v1 = f16_to_f32(x16[o + 1]);
+    wave_had_pre(v0, v1, f16_to_f32(sv[0]), f16_to_f32(sv[1]));
+  } else {
+    v0 = x32[o];
+    v1 = x32[o + 1];
+    wave_had_post(v0, v1, f16_to_f32(sv[0]), f16_to_f32(sv[1]));
+  }
+  y[o] = f32_to_f16(v0);
+  y[o + 1] = f32_to_f16(v1);
+}
+
+// ---------------------------------------------------------------------------------
+// QMV: grid (n_cb * S, row passes, members); 4 waves per workgroup. Workgroup (cb, s)
+// owns output columns [cb*128, cb*128+128) and k-tiles [s*4T, s*4T + 4T); wave w takes
+// the T consecutive k-tiles starting at s*4T + w*T. Output: f32 partials
+// part[member][s][row][col], each the in-order sum of the four waves' partials.
+// ---------------------------------------------------------------------------------
+template <int K, int CB, int MB>
+__global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_n, int in,
+                                             int out, int T, int S,
+                                             const uint16_t *__restrict__ xhat,
+                                             int64_t x_member_stride, int64_t rows,
+                                             float *__restrict__ part) {
+  __shared__ uint32_t xs[MB * kQmvMaxKtPerWg * 8];
+  __shared__ float red[kQmvWaves * MB * 128];
+  const int n_cb = out / 128;
+  const int cb = blockIdx.x % n_cb, s = blockIdx.x / n_cb;
+  const int64_t r0 = (int64_t)blockIdx.y * MB;
+  const int member = blockIdx.z;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kt_wg = kQmvWaves * T;
+  const int k0 = s * kt_wg;
+
+  const uint16_t *xm = xhat + member * x_member_stride;
+  for (int i = threadIdx.x; i < MB * kt_wg * 8; i += 256) {
+    const int r = i / (kt_wg * 8), wd = i % (kt_wg * 8);
+    uint32_t v = 0;
+    if (r0 + r < rows) v = reinterpret_cast<const uint32_t *>(xm + (r0 + r) * in + k0 * 16)[wd];
+    xs[r * kQmvMaxKtPerWg * 8 + wd] = v;
+  }
+  __syncthreads();
+
+  float acc[MB][2];
+  qmv_wave_loop<K, CB, MB>((const uint32_t *)trellis.p[member], tiles_n, cb * 8 + (lane >> 3),
+                           lane & 7, k0 + wave * T, T, wave, xs, acc);
+  qmv_stash<MB>(red, wave, lane, acc);
+  __syncthreads();
+  for (int i = threadIdx.x; i < MB * 128; i += 256) {
+    const int r = i >> 7, c = i & 127;
+    if (r0 + r >= rows) continue;
+    part[(((int64_t)member * S + s) * rows + r0 + r) * out + cb * 128 + c] =
+        qmv_wave_sum<MB>(red, r, c);
+  }
+}
+
+// One wave per (member, row, 128-column block): split sum in split order, then the raw
+// f32 result or the output Hadamard.
+__global__ __launch_bounds__(256) void k_qmv_finalize(int n, int S, int64_t rows, int out,
+                                                      const float *__restrict__ part,
+                                                      float *__restrict__ y32,
+                                                      uint16_t *__restrict__ y16,
+                                                      exl3h::PtrTable svh) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n_cb = out / 128;
+  if (gw >= (int64_t)n * rows * n_cb) return;
+  const int cb = (int)(gw % n_cb);
+  const int64_t rest = gw / n_cb;
+  const int64_t row = rest % rows;
+  const int member = (int)(rest / rows);
+  const int c = cb * 128 + 2 * lane;
+  float v0 = 0.0f, v1 = 0.0f;
+  for (int s = 0; s < S; ++s) {
+    const float *p = part + (((int64_t)member * S + s) * rows + row) * out + c;
+    if (s == 0) {
+      v0 = p[0];
+      v1 = p[1];
+    } else {
+      v0 += p[0];
+      v1 += p[1];
+    }
+  }
+  const int64_t o = ((int64_t)member * rows + row) * out + c;
+  if (y32) {
+    y32[o] = v0;
+    y32[o + 1] = v1;
+    return;
+  }
+  const uint16_t *sv = (const uint16_t *)svh.p[member] + c;
+  wave_had_post(v0, v1, f16_to_f32(sv[0]), f16_to_f32(sv[1]));
+  y16[o] = f32_to_f16(v0);
+  y16[o + 1] = f32_to_f16(v1);
+}
+
+}  // namespace
+
+namespace exl3h {
+
+exl3_status launch_decode(const exl3_trellis_desc &w, uint16_t *w_hat, hipStream_t st) {
+  const int tiles_n = w.out_features / 16, tiles_k = w.in_features / 16;
+  dim3 grid(tiles_n, tiles_k);
+  const uint32_t *t = (const uint32_t *)w.trellis;
+  switch (w.codebook) {
+    case 0: k_decode<0><<<grid, 256, 0, st>>>(t, w.K, tiles_n, w.out_features, w_hat); break;
+    case 1: k_decode<1><<<grid, 256, 0, st>>>(t, w.K, tiles_n, w.out_features, w_hat); break;
+    default: k_decode<2><<<grid, 256, 0, st>>>(t, w.K, tiles_n, w.out_features, w_hat); break;
+  }
+  EXL3_LAUNCHED("k_decode");
+  return EXL3_OK;
+}
+
+exl3_status launch_reconstruct(const exl3_trellis_desc &w, uint16_t *w_out, hipStream_t st) {
+  const int tiles_n = w.out_features / 16;
+  dim3 grid(w.out_features / 128, w.in_features / 128);
+  const uint32_t *t = (const uint32_t *)w.trellis;
+  switch (w.codebook) {
+    case 0:
+      k_reconstruct<0><<<grid, 256, 0, st>>>(t, w.K, tiles_n, w.out_features, w.suh, w.svh, w_out);
+      break;
+    case 1:
+      k_reconstruct<1><<<grid, 256, 0, st>>>(t, w.K, tiles_n, w.out_features, w.suh, w.svh, w_out);
+      break;
+    default:
+      k_reconstruct<2><<<grid, 256, 0, st>>>(t, w.K, tiles_n, w.out_features, w.suh, w.svh, w_out);
+      break;
+  }
+  EXL3_LAUNCHED("k_reconstruct");
+  return EXL3_OK;
+}
+
+exl3_status launch_hadamard(const uint16_t *x16, const float *x32, int64_t rows, int n,
+                            const PtrTable &s, int64_t rows_per_member, uint16_t *y,
+                            hipStream_t st) {
+  const int64_t waves = rows * (n / 128);
+  if (waves == 0) return EXL3_OK;
+  k_hadamard<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(x16, x32, rows, n, s, rows_per_member, y);
+  EXL3_LAUNCHED("k_hadamard");
+  return EXL3_OK;
+}
+
+template <int K, int CB, int MB>
+static void qmv_go(dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in, int out,
+                   int T, int S, const uint16_t *xhat, int64_t xs, int64_t rows, float *part) {
+  k_qmv<K, CB, MB><<<grid, 256, 0, st>>>(tr, tiles_n, in, out, T, S, xhat, xs, rows, part);
+}
+
+template <int K, int CB>
+static void qmv_mb(int mb, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in,
+                   int out, int T, int S, const uint16_t *xhat, int64_t xs, int64_t rows,
+                   float *part) {
+  switch (mb) {
+    case 1: qmv_go<K, CB, 1>(grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
+    case 2: qmv_go<K, CB, 2>(grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
+    default: qmv_go<K, CB, 4>(grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
+  }
+}
+
+template <int K>
+static void qmv_cb(int cb, int mb, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n,
+                   int in, int out, int T, int S, const uint16_t *xhat, int64_t xs, int64_t rows,
+                   float *part) {
+  switch (cb) {
+    case 0: qmv_mb<K, 0>(mb, grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
+    case 1: qmv_mb<K, 1>(mb, grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
+    default: qmv_mb<K, 2>(mb, grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
+  }
+}
+
+exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, int n,
+                       const uint16_t *xhat, int64_t x_member_stride, int64_t rows, float *part,
+                       hipStream_t st) {
+  const int in = shape.in_features, out = shape.out_features;
+  const KPart kp = kpart(in / 16);
+  const exl3_tuning tn = tuning();
+  int mb = tn.rows_per_pass > 0 ? tn.rows_per_pass : (rows >= 4 ? 4 : (int)rows);
+  mb = mb >= 4 ? 4 : (mb >= 2 ? 2 : 1);
+  dim3 grid((unsigned)((out / 128) * kp.S), (unsigned)((rows + mb - 1) / mb), (unsigned)n);
+  const int tiles_n = out / 16;
+  switch (shape.K) {
+#define EXL3_K(KK)                                                                        \
+  case KK:                                                                                \
+    qmv_cb<KK>(shape.codebook, mb, grid, st, trellis, tiles_n, in, out, kp.T, kp.S, xhat,  \
+               x_member_stride, rows, part);                                              \
+    break;
+    EXL3_K(1) EXL3_K(2) EXL3_K(3) EXL3_K(4) EXL3_K(5) EXL3_K(6) EXL3_K(7) EXL3_K(8)
+#undef EXL3_K
+    default: return fail(EXL3_ERR_INVALID, "K out of range");
+  }
+  EXL3_LAUNCHED("k_qmv");
+  return EXL3_OK;
+}
+
+exl3_status launch_qmv_finalize(int n, int S, int64_t rows, int out, const float *part,
+                                float *y32, uint16_t *y16, const PtrTable &svh, hipStream_t st) {
+  const int64_t waves = (int64_t)n * rows * (out / 128);
+  if (waves == 0) return EXL3_OK;
+  k_qmv_finalize<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(n, S, rows, out, part, y32, y16, svh);
+  EXL3_LAUNCHED("k_qmv_finalize");
+  return EXL3_OK;
+}
+
+}  // namespace exl3h

@@ -1,0 +1,264 @@
+/*
+ * exl3_moe.h -- C ABI of the MI355X (gfx950) EXL3 trellis / GLM-5 MoE decode library.
+ *
+ * Drop-in boundary for the reference's trellis_gemm.h / glm5_moe.h call surface
+ * (muyouming/exl3-server): the same EXL3 tensors (.trellis words, .suh/.svh f16
+ * scales, K bits, codebook) and the same (rows, hidden) f16 activations in, the same
+ * f16 results out. Plain pointers and sizes only; every device pointer is caller-owned
+ * HIP device memory; every call is asynchronous on the given stream (a hipStream_t,
+ * NULL = the default stream) unless stated otherwise.
+ *
+ * Errors: every entry point returns an exl3_status; exl3_last_error() describes the
+ * last failure on the calling thread. Nothing is thrown across the ABI. Shape and
+ * geometry errors are detected on the host before any kernel is launched.
+ *
+ * Threading: calls are thread-safe for distinct streams and distinct handles. A layer
+ * handle and its workspace must not be used by two in-flight calls at once (the
+ * workspace holds that call's intermediate state and completion counters).
+ */
+#ifndef EXL3_MOE_H
+#define EXL3_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *exl3_stream_t; /* hipStream_t */
+
+typedef enum {
+  EXL3_OK = 0,
+  EXL3_ERR_INVALID = 1,     /* bad argument, shape or geometry */
+  EXL3_ERR_UNSUPPORTED = 2, /* valid input outside what this build implements */
+  EXL3_ERR_WORKSPACE = 3,   /* workspace missing or smaller than the size query */
+  EXL3_ERR_HIP = 4,         /* a HIP runtime call failed */
+} exl3_status;
+
+/* Codebook ids as the reference (exl3.h:28; loader glm5.cpp:303). */
+typedef enum { EXL3_CB_3INST = 0, EXL3_CB_MCG = 1, EXL3_CB_MUL1 = 2 } exl3_codebook;
+
+/* One EXL3 trellis tensor. Replaces TrellisWeight (trellis_gemm.h:21-48).
+ * `trellis` is the on-disk (in/16, out/16, 16*K) int16 array as bytes: tile
+ * (tk, tn) starts at byte (tk*(out/16) + tn)*32*K and holds 8*K little-endian
+ * 32-bit ring words. The base must be 4-byte aligned (the reference's unaligned
+ * byte path, trellis_gemm.cpp:311-316, is a loader concern: use exl3_trellis_pack).
+ * in/out must be multiples of 128 (Hadamard blocks); 1 <= K <= 8. */
+typedef struct {
+  const void *trellis;  /* device */
+  const uint16_t *suh;  /* device f16 [in_features] */
+  const uint16_t *svh;  /* device f16 [out_features] */
+  int32_t in_features;
+  int32_t out_features;
+  int32_t K;
+  int32_t codebook;     /* exl3_codebook */
+} exl3_trellis_desc;
+
+/* A linear of the MoE: trellis, or plain f16 (in, out) row-major when dense != NULL.
+ * Replaces G5Linear (glm5.h:41-49; biases are not used by the MoE). */
+typedef struct {
+  exl3_trellis_desc tw;    /* used when dense == NULL */
+  const uint16_t *dense;   /* device f16 (in_features, out_features) or NULL */
+  int32_t in_features;
+  int32_t out_features;
+} exl3_linear_desc;
+
+/* MoE fields of ModelConfig (model.h:47-53, 68-69; parsed model.cpp:138-144,160-161). */
+typedef struct {
+  int32_t hidden_size;
+  int32_t moe_intermediate_size;
+  int32_t n_routed_experts;
+  int32_t num_experts_per_tok;
+  int32_t n_group;          /* routing groups (1 = none) */
+  int32_t topk_group;       /* groups kept */
+  int32_t norm_topk_prob;   /* bool */
+  float routed_scaling_factor;
+  float swiglu_limit;       /* 0 = no clamp */
+} exl3_moe_config;
+
+/* The MoE weights of one layer. Replaces G5Layer's MoE members (glm5.h:104-110):
+ * experts[3*e + {0,1,2}] = gate, up, down of expert e (host array of descriptors
+ * pointing at device tensors), shared[0..2] = shared expert gate/up/down or NULL,
+ * router_w = gate.weight (E, hidden) f16, router_bias = e_score_correction_bias (E) f32. */
+typedef struct {
+  const exl3_linear_desc *experts;  /* host array, 3 * n_routed_experts entries */
+  const exl3_linear_desc *shared;   /* host array of 3, or NULL */
+  const uint16_t *router_w;         /* device f16 (E, hidden) */
+  const float *router_bias;         /* device f32 (E) */
+} exl3_moe_layer_desc;
+
+/* Scheduling knobs. Mirrors TrellisTuning (trellis_gemm.h:137-145): rows_per_pass is
+ * the QMV row block (reference mb), mat_min_rows the staged-MFMA threshold (0 = off,
+ * default 16), mat_max_rows its cap (0 = none). None of them changes an output bit
+ * of the QMV path (the k-split partition is a function of the tensor shape only). */
+typedef struct {
+  int32_t rows_per_pass;  /* 0 = auto (min(rows, 4)) */
+  int32_t mat_min_rows;   /* staged fp16 MFMA path for runs with >= this many rows */
+  int32_t mat_max_rows;   /* 0 = no cap */
+} exl3_tuning;
+
+/* What a trellis linear at `rows` rows will do. Mirrors TrellisPathInfo
+ * (trellis_gemm.h:154-162). passes = weight streams per call. */
+typedef struct {
+  int32_t staged;
+  int32_t rows_per_block;
+  int32_t pad_rows;
+  int32_t passes;
+  int32_t splits;
+  int32_t tiles_per_workgroup;
+} exl3_path_info;
+
+/* Per-layer dispatch statistics. Mirrors MoeRowsDiag (glm5_moe.h:112-122) plus the
+ * run-length histogram the reference prints under EXL3_MOE_RUNS_DEBUG
+ * (glm5_moe.cpp:288-295). Collected only while enabled (it synchronises the stream
+ * after each layer call to read the device-side run table). */
+typedef struct {
+  int64_t calls;
+  int64_t pairs;
+  int64_t runs;
+  int64_t distinct_experts;
+  int64_t staged_runs;
+  int64_t streamed_bytes;
+  int64_t shared_bytes;
+  int64_t run_hist[65];  /* run_hist[r] = runs of r rows (r >= 64 counted at 64) */
+} exl3_moe_diag;
+
+/* Per-stage GPU time of the layer calls made while timing is enabled (HIP events on
+ * the call's stream around each stage; the call synchronises its stream at the end).
+ * The counterpart of the reference's Glm5Profile / moe_bench stage timing
+ * (glm5_forward.h:53-66, moe_bench.cpp:444-462). Bytes are the EXL3 trellis bytes of
+ * the distinct experts each call streamed (each expert counted once per call). */
+typedef struct {
+  int64_t calls;
+  double router_ms;     /* logits + top-k routing + expert-order dispatch */
+  double shared_ms;     /* shared expert */
+  double gate_up_ms;    /* routed gate|up + SwiGLU kernel */
+  double down_ms;       /* routed down + weighted combine kernel */
+  double total_ms;
+  int64_t gate_up_trellis_bytes;
+  int64_t down_trellis_bytes;
+} exl3_moe_timing;
+
+typedef struct exl3_moe_layer_s *exl3_moe_layer_t;
+
+/* ---- library ------------------------------------------------------------------ */
+
+const char *exl3_last_error(void);
+/* Version of this ABI (bumped on any incompatible change). */
+int32_t exl3_abi_version(void);
+
+/* Replaces trellis_set_tuning / trellis_get_tuning (trellis_gemm.h:144-145). */
+exl3_status exl3_set_tuning(const exl3_tuning *t);
+exl3_status exl3_get_tuning(exl3_tuning *t);
+/* Replaces trellis_path_info (trellis_gemm.h:162). */
+exl3_status exl3_trellis_path_info(const exl3_trellis_desc *w, int64_t rows,
+                                   exl3_path_info *info);
+
+/* ---- single trellis tensor ---------------------------------------------------- */
+
+/* Copy on-disk words (host, (k_tiles, n_tiles, 16K) int16) to a 4-byte-aligned device
+ * buffer of k_tiles*n_tiles*32*K bytes. Replaces trellis_pack (trellis_gemm.h:64). */
+exl3_status exl3_trellis_pack(const uint16_t *words16_host, int32_t k_tiles, int32_t n_tiles,
+                              int32_t K, void *dst_device, exl3_stream_t stream);
+
+/* W_hat, the decoded rotated-basis weight, f16 row-major [in, out]. Bit-exact with
+ * exl3::decode_inner (exl3.h:44; exl3.cpp:109-125). Only needs in/out % 16 == 0. */
+exl3_status exl3_trellis_decode(const exl3_trellis_desc *w, uint16_t *w_hat,
+                                exl3_stream_t stream);
+
+/* W = diag(suh) H W_hat H diag(svh) / 128, f16 [in, out]. Bit-exact with
+ * exl3::reconstruct (exl3.h:48; exl3.cpp:152-209). */
+exl3_status exl3_trellis_reconstruct(const exl3_trellis_desc *w, uint16_t *w_out,
+                                     exl3_stream_t stream);
+
+/* One Hadamard step of the linear. Replaces trellis_hadamard (trellis_gemm.h:77-78):
+ *   pre  (x_f16 != NULL): y = f16(H128(f32(x) * f32(s)) / sqrt(128))
+ *   post (x_f32 != NULL): y = f16(H128(f32(f16(x))) / sqrt(128) * f32(s))
+ * Exactly one of x_f16 / x_f32 is non-NULL. x is (rows, n), s is f16 [n] or, when
+ * stacked > 0, `stacked` member vectors [stacked, n] with rows/stacked rows each. */
+exl3_status exl3_trellis_hadamard(const uint16_t *x_f16, const float *x_f32, int64_t rows,
+                                  int32_t n, const uint16_t *s, int32_t stacked, uint16_t *y,
+                                  exl3_stream_t stream);
+
+/* Workspace bytes for exl3_trellis_matmul_raw / exl3_trellis_linear(_grouped) on
+ * n_members members of w's shape at `rows` rows. */
+size_t exl3_trellis_workspace_size(const exl3_trellis_desc *w, int64_t rows, int32_t n_members);
+
+/* yhat = xhat @ W_hat (f32, (rows, out)); xhat already rotated. Replaces
+ * trellis_matmul_raw (trellis_gemm.h:68). */
+exl3_status exl3_trellis_matmul_raw(const exl3_trellis_desc *w, const uint16_t *xhat,
+                                    int64_t rows, float *yhat, void *workspace,
+                                    size_t workspace_bytes, exl3_stream_t stream);
+
+/* y = x @ W, f16 (rows, in) -> f16 (rows, out). Replaces trellis_linear
+ * (trellis_gemm.h:51; trellis_gemm.cpp:1157-1197). */
+exl3_status exl3_trellis_linear(const exl3_trellis_desc *w, const uint16_t *x, int64_t rows,
+                                uint16_t *y, void *workspace, size_t workspace_bytes,
+                                exl3_stream_t stream);
+
+/* n linears of one shape in one launch, no member cap. members: host array of n.
+ * x is (n, rows, in) (x_shared = 0, replaces trellis_linear_group_rows) or one
+ * (rows, in) block shared by every member (x_shared = 1, replaces
+ * trellis_linear_group); y is (n, rows, out). suh_stack/svh_stack, when non-NULL,
+ * are device (n, in)/(n, out) f16 stacks used instead of the members' own scales
+ * (replaces the *_scaled forms, trellis_gemm.h:102-106). Bit-identical to n calls
+ * of exl3_trellis_linear. */
+exl3_status exl3_trellis_linear_grouped(const exl3_trellis_desc *members, int32_t n,
+                                        const uint16_t *x, int64_t rows, int32_t x_shared,
+                                        const uint16_t *suh_stack, const uint16_t *svh_stack,
+                                        uint16_t *y, void *workspace, size_t workspace_bytes,
+                                        exl3_stream_t stream);
+
+/* ---- MoE layer ---------------------------------------------------------------- */
+
+/* Validates a layer (every expert of a projection class must share shape, K and
+ * codebook; moe_prep_of, glm5_moe.cpp:430-486) and uploads its device-resident
+ * expert table (pointer and scale tables, the G5MoePrep equivalent). Synchronous.
+ * The weights themselves are referenced, not copied. */
+exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_moe_config *cfg,
+                                  exl3_moe_layer_t *out);
+exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer);
+
+/* Workspace bytes for a call with `rows` (= B * L) token rows. */
+size_t exl3_moe_workspace_size(exl3_moe_layer_t layer, int64_t rows);
+
+/* Router only: weights (rows, top_k) f32 and ids (rows, top_k) i32 from h (rows, hidden)
+ * f16. Replaces the logits matmul + moe_topk_route (glm5_moe.cpp:16-60, 127-130).
+ * Ids are in descending scores-for-choice order (ties: lower id first). */
+exl3_status exl3_moe_route(exl3_moe_layer_t layer, const uint16_t *h, int64_t rows,
+                           float *weights, int32_t *ids, void *workspace,
+                           size_t workspace_bytes, exl3_stream_t stream);
+
+/* Routing from caller logits (rows, n_experts) f32 and bias (n_experts) f32, no layer
+ * handle. Replaces moe_topk_route (glm5_moe.h:29-31; glm5_moe.cpp:16-60): sigmoid
+ * scores, bias used for selection only, optional group limit (n_group/topk_group:
+ * group score = sum of its top-2 biased scores), top_k by biased score (ties: lower
+ * id), weights = un-biased scores, normalised when norm_topk_prob, times
+ * routed_scaling_factor. Only the routing fields of cfg are read. */
+exl3_status exl3_moe_topk_route(const float *logits, const float *bias, int64_t rows,
+                                const exl3_moe_config *cfg, float *weights, int32_t *ids,
+                                exl3_stream_t stream);
+
+/* The whole routed + shared MoE block: out (B, L, hidden) f16 from h (B, L, hidden)
+ * f16. Replaces moe_layer (glm5_moe.h:35) and moe_layer_rows (glm5_moe.h:97); no host
+ * round trip: routing, dispatch and every expert launch stay on the device. */
+exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B, int64_t L,
+                           uint16_t *out, void *workspace, size_t workspace_bytes,
+                           exl3_stream_t stream);
+
+/* Stage timing (exl3_moe_timing); enabling it makes each layer call synchronous. */
+exl3_status exl3_moe_timing_enable(exl3_moe_layer_t layer, int32_t enabled);
+exl3_status exl3_moe_timing_get(exl3_moe_layer_t layer, exl3_moe_timing *out);
+exl3_status exl3_moe_timing_reset(exl3_moe_layer_t layer);
+
+/* MoeRowsDiag equivalents (glm5_moe.h:121-122). */
+exl3_status exl3_moe_diag_enable(exl3_moe_layer_t layer, int32_t enabled);
+exl3_status exl3_moe_diag_get(exl3_moe_layer_t layer, exl3_moe_diag *out);
+exl3_status exl3_moe_diag_reset(exl3_moe_layer_t layer);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_MOE_H */

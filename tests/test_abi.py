@@ -1,0 +1,94 @@
+"""CPU tests of the C ABI boundary: the library loads, exports every symbol the header
+declares, and host-side validation answers without touching a GPU."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from exl3_amd import _lib
+from exl3_amd._lib import TrellisDesc
+
+
+def test_library_exports_every_header_symbol():
+    L = _lib.lib()
+    syms = _lib.header_symbols()
+    assert len(syms) >= 20
+    for s in syms:
+        assert hasattr(L, s), s
+    # the Python binding declares a signature for each of them
+    assert sorted(_lib.SIGNATURES) == syms
+
+
+def test_abi_version_and_tuning_roundtrip():
+    L = _lib.lib()
+    assert L.exl3_abi_version() == 1
+    t0 = _lib.Tuning()
+    _lib.call("exl3_get_tuning", C.byref(t0))
+    assert t0.mat_min_rows == 16
+    _lib.call("exl3_set_tuning", C.byref(_lib.Tuning(2, 0, 0)))
+    t1 = _lib.Tuning()
+    _lib.call("exl3_get_tuning", C.byref(t1))
+    assert (t1.rows_per_pass, t1.mat_min_rows) == (2, 0)
+    _lib.call("exl3_set_tuning", C.byref(t0))
+
+
+def fake_desc(in_f=4096, out_f=1024, K=4, cb=1, base=0x10000):
+    # never dereferenced: only host-side validation runs in these tests
+    return TrellisDesc(base, base + 0x100000, base + 0x200000, in_f, out_f, K, cb)
+
+
+def test_validation_errors_without_gpu():
+    L = _lib.lib()
+    info = _lib.PathInfo()
+    for bad in (fake_desc(K=0), fake_desc(K=9), fake_desc(cb=3), fake_desc(in_f=100),
+                fake_desc(out_f=0), fake_desc(base=0x10002)):
+        st = L.exl3_trellis_path_info(C.byref(bad), 1, C.byref(info))
+        assert st == _lib.EXL3_ERR_INVALID
+        assert L.exl3_last_error()
+    with pytest.raises(_lib.Exl3Error) as ei:
+        _lib.call("exl3_trellis_linear", C.byref(fake_desc(K=11)), 0x1000, 1, 0x2000, None, 0,
+                  None)
+    assert ei.value.status == _lib.EXL3_ERR_INVALID
+    assert b"K must be" in L.exl3_last_error()
+
+
+def test_path_info_and_workspace_query():
+    L = _lib.lib()
+    info = _lib.PathInfo()
+    d = fake_desc()
+    _lib.call("exl3_trellis_path_info", C.byref(d), 8, C.byref(info))
+    assert info.staged == 0 and info.rows_per_block == 4 and info.passes == 2
+    assert info.splits == 4  # 256 k-tiles: 4 waves x 16 k-tiles x 4 splits
+    ws1 = L.exl3_trellis_workspace_size(C.byref(d), 1, 1)
+    ws8 = L.exl3_trellis_workspace_size(C.byref(d), 8, 3)
+    assert 0 < ws1 < ws8
+    assert ws1 >= 4096 * 2 + 4 * 1024 * 4  # xhat + 4 split planes
+
+
+def test_workspace_too_small_is_reported_before_launch():
+    L = _lib.lib()
+    d = fake_desc()
+    st = L.exl3_trellis_linear(C.byref(d), 0x1000, 1, 0x2000, 0x100000, 16, None)
+    assert st == _lib.EXL3_ERR_WORKSPACE
+
+
+def test_topk_route_rejects_bad_config():
+    L = _lib.lib()
+    cfg = _lib.MoeConfig(0, 0, 5, 6, 1, 1, 1, 1.0, 0.0)  # top_k > E
+    st = L.exl3_moe_topk_route(0x1000, 0x2000, 1, C.byref(cfg), 0x3000, 0x4000, None)
+    assert st == _lib.EXL3_ERR_INVALID
+    cfg = _lib.MoeConfig(0, 0, 2048, 8, 1, 1, 1, 1.0, 0.0)  # too many experts
+    assert L.exl3_moe_topk_route(0x1000, 0x2000, 1, C.byref(cfg), 0x3000, 0x4000,
+                                 None) == _lib.EXL3_ERR_UNSUPPORTED
+
+
+def test_synth_generator_is_counter_based():
+    from exl3_amd import synth
+    a = synth.trellis_words(1, "t", 32, 64, 3)
+    b = synth.trellis_words(1, "t", 32, 64, 3)
+    c = synth.trellis_words(1, "u", 32, 64, 3)
+    assert a.shape == (2, 4, 48) and np.array_equal(a, b) and not np.array_equal(a, c)
+    # uniform 16-bit words: mean near 32767.5
+    assert abs(a.astype(np.float64).mean() - 32767.5) < 2000
+    x = synth.normal(2, "n", (100000,))
+    assert abs(x.mean()) < 0.02 and abs(x.std() - 1) < 0.02

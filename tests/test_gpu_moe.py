@@ -1,0 +1,259 @@
+"""GPU parity tests of the MoE layer through the C ABI.
+
+Routing: top-k id sets equal to the oracle's f64 routing, except where the k-th and
+(k+1)-th biased scores are closer than NEAR_TIE (reported, then the oracle's routing
+is used to check the experts' arithmetic). Layer output: the north-star tolerance,
+max |err| <= 2e-2 * rms(reference) and cosine >= 0.9999.
+Invariants of the reference (moe_test.cpp (g)/(h)): an N-row call equals N single-row
+calls bit for bit; the run grouping equals the oracle's.
+"""
+import numpy as np
+import pytest
+import torch
+
+from exl3_amd import synth
+from exl3_amd.moe import DeviceMoeLayer, moe_topk_route, trellis_words_torch
+
+pytestmark = pytest.mark.gpu
+
+NEAR_TIE = 1e-6
+TOL_RMS = 2e-2
+COS_MIN = 0.9999
+
+
+def ocfg_of(oracle, cfg, has_shared):
+    return oracle.make_cfg(cfg.hidden, cfg.inter, cfg.n_experts, cfg.top_k, cfg.n_group,
+                           cfg.topk_group, cfg.norm_topk_prob, has_shared,
+                           cfg.routed_scaling_factor, cfg.swiglu_limit)
+
+
+def to_dev(h_bits, dev, B, L, H):
+    return torch.from_numpy(h_bits.view(np.float16)).to(dev).view(B, L, H)
+
+
+def check_out(got_t, want_bits):
+    got = got_t.float().cpu().numpy().astype(np.float64).reshape(want_bits.shape)
+    ref = want_bits.view(np.float16).astype(np.float64)
+    rms = np.sqrt(np.mean(ref ** 2))
+    err = np.max(np.abs(got - ref))
+    cos = (got * ref).sum() / np.sqrt((got ** 2).sum() * (ref ** 2).sum())
+    assert np.isfinite(got).all() and rms > 1e-3
+    assert err <= TOL_RMS * rms, (err, rms)
+    assert cos >= COS_MIN, cos
+    return err / rms, cos
+
+
+def check_routing(oracle, logits, bias, ids_gpu, cfg):
+    """Set equality per row, allowing only near-tie flips at the k-th boundary."""
+    idx, w = oracle.route(logits, bias, cfg)
+    sc = 1 / (1 + np.exp(-logits))
+    sfc = sc + bias.astype(np.float64)[None, :]
+    K = cfg.top_k
+    flips = 0
+    for b in range(idx.shape[0]):
+        if set(ids_gpu[b].tolist()) == set(idx[b].tolist()):
+            continue
+        s = np.sort(sfc[b])[::-1]
+        assert s[K - 1] - s[K] < NEAR_TIE, f"row {b}: routing differs without a near tie"
+        flips += 1
+    return idx, w, flips
+
+
+def test_topk_route_known_answers(dev):
+    # tests/moe_test.cpp:225-254: bias flips the selection to {0, 3}
+    logits = torch.tensor([[2.0, 1.0, 0.5, -2.0, -3.0]], device=dev)
+    bias = torch.tensor([0.0, 0.0, 0.0, 0.8, 0.75], device=dev)
+    w, ids = moe_topk_route(logits, bias, 1, 1, 2, True, 2.5)
+    got = dict(zip(ids[0].tolist(), w[0].tolist()))
+    assert sorted(got) == [0, 3]
+    assert abs(got[0] - 2.201993) < 1e-4 and abs(got[3] - 0.298008) < 1e-4
+    # tests/moe_test.cpp:256-275: group limit selects {0, 1}
+    w, ids = moe_topk_route(torch.tensor([[1.0, 0.9, 2.0, -1.0]], device=dev),
+                            torch.zeros(4, device=dev), 2, 1, 2, False, 1.0)
+    assert sorted(ids[0].tolist()) == [0, 1]
+
+
+def test_topk_route_vs_oracle_many_rows(oracle, dev):
+    rng = np.random.default_rng(3)
+    E, K = 288, 8
+    lg = rng.normal(scale=0.5, size=(300, E)).astype(np.float32)
+    b = rng.normal(scale=0.01, size=E).astype(np.float32)
+    w, ids = moe_topk_route(torch.from_numpy(lg).to(dev), torch.from_numpy(b).to(dev), 1, 1, K,
+                            True, 2.5)
+    cfg = oracle.make_cfg(16, 16, E, K, 1, 1, True, False, 2.5, 10.0)
+    idx, ow, flips = check_routing(oracle, lg.astype(np.float64), b, ids.cpu().numpy(), cfg)
+    assert flips == 0
+    # weights in the oracle's order, f32 vs f64
+    got = np.take_along_axis(w.cpu().numpy(), np.argsort(ids.cpu().numpy(), 1), 1)
+    want = np.take_along_axis(ow, np.argsort(idx, 1), 1)
+    assert np.allclose(got, want, rtol=2e-6, atol=1e-7)
+    # groups: 8 groups of 36, keep 4
+    cfg_g = oracle.make_cfg(16, 16, E, K, 8, 4, True, False, 2.5, 10.0)
+    w, ids = moe_topk_route(torch.from_numpy(lg).to(dev), torch.from_numpy(b).to(dev), 8, 4, K,
+                            True, 2.5)
+    idx, _ = oracle.route(lg.astype(np.float64), b, cfg_g)
+    assert np.array_equal(np.sort(ids.cpu().numpy(), 1), np.sort(idx, 1))
+
+
+@pytest.mark.parametrize("B", [1, 4, 8, 17])
+def test_small_layer_vs_oracle(oracle, dev, B):
+    # configs[0]'s layer (hidden 512, 16 experts, top-2, K4 mcg, no shared expert)
+    cfg = synth.config_small()
+    layer = synth.make_layer(cfg, 2024)
+    h = synth.activations(2024, f"small.x.{B}", B, cfg.hidden)
+    d = DeviceMoeLayer(layer, dev)
+    y = d(to_dev(h, dev, B, 1, cfg.hidden))
+    _, ids = d.route(to_dev(h, dev, B, 1, cfg.hidden))
+    oc = ocfg_of(oracle, cfg, False)
+    logits = oracle.router_logits(h, layer.router_w)
+    idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+    want = oracle.moe_layer_routed(oc, [l.oracle_dict() for l in layer.experts], None, h, idx, w)
+    check_out(y, want)
+    d.close()
+
+
+def test_layer_with_shared_experts(oracle, dev):
+    # trellis shared expert (configs[4]'s mix, small) and an f16 shared expert
+    for shared_K in (6, 0):
+        cfg = synth.MoeConfig(hidden=512, inter=256, n_experts=24, top_k=4, routed_scaling_factor=2.5,
+                              shared_inter=384, gate_up_K=4, gate_up_cb=0, down_K=5, down_cb=2,
+                              shared_K=shared_K, shared_cb=1)
+        layer = synth.make_layer(cfg, 99)
+        B = 6
+        h = synth.activations(99, "sh.x", B, cfg.hidden)
+        d = DeviceMoeLayer(layer, dev)
+        y = d(to_dev(h, dev, B, 1, cfg.hidden))
+        _, ids = d.route(to_dev(h, dev, B, 1, cfg.hidden))
+        oc = ocfg_of(oracle, cfg, True)
+        logits = oracle.router_logits(h, layer.router_w)
+        idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+        want = oracle.moe_layer_routed(oc, [l.oracle_dict() for l in layer.experts],
+                                       [l.oracle_dict() for l in layer.shared], h, idx, w)
+        check_out(y, want)
+        d.close()
+
+
+def test_rows_path_equals_single_rows(dev):
+    # moe_test.cpp (g)/(h): 128-wide fixture, 4 experts, top-3, 11 rows (33 pairs,
+    # every expert selected several times); the batch equals single-row calls
+    cfg = synth.MoeConfig(hidden=128, inter=128, n_experts=4, top_k=3, routed_scaling_factor=1.5,
+                          gate_up_K=3, gate_up_cb=2, down_K=3, down_cb=2, shared_inter=128,
+                          shared_K=3, shared_cb=2)
+    layer = synth.make_layer(cfg, 5)
+    d = DeviceMoeLayer(layer, dev)
+    for B in (4, 11):
+        h = synth.activations(5, f"rows.{B}", B, 128)
+        x = to_dev(h, dev, B, 1, 128)
+        yb = d(x).cpu()
+        assert torch.isfinite(yb.float()).all() and yb.float().abs().max() > 1e-3
+        for b in range(B):
+            yo = d(x[b:b + 1].contiguous()).cpu()
+            assert torch.equal(yo.view(-1), yb[b].view(-1)), b
+    d.close()
+
+
+def test_repeat_calls_are_deterministic(dev):
+    cfg = synth.config_small()
+    layer = synth.make_layer(cfg, 7)
+    d = DeviceMoeLayer(layer, dev)
+    h = synth.activations(7, "det", 8, cfg.hidden)
+    x = to_dev(h, dev, 8, 1, cfg.hidden)
+    y0 = d(x).clone()
+    for _ in range(5):
+        assert torch.equal(d(x), y0)
+    d.close()
+
+
+def glm5_layer_on_device(dev, seed, tag):
+    """Full-size GLM-5 layer: small tensors from numpy, trellis words on the device."""
+    cfg = synth.config_glm5()
+    H, I, E = cfg.hidden, cfg.inter, cfg.n_experts
+    layer = synth.MoeLayer(cfg, [], None, synth.normal_f16(seed, f"{tag}.gate.weight", (E, H), 0, 0.02),
+                           synth.normal_f32(seed, f"{tag}.gate.e_score_correction_bias", (E,), 0, 0.01))
+    words = {}
+    for e in range(E):
+        for j, (nm, i_f, o_f, K) in enumerate((("gate_proj", H, I, cfg.gate_up_K),
+                                               ("up_proj", H, I, cfg.gate_up_K),
+                                               ("down_proj", I, H, cfg.down_K))):
+            p = f"{tag}.experts.{e}.{nm}"
+            lin = synth.Linear(i_f, o_f, trellis=None, suh=synth.normal_f16(seed, p + ".suh", (i_f,), 1, 0.05),
+                               svh=synth.normal_f16(seed, p + ".svh", (o_f,), 1, 0.05), K=K,
+                               cb=cfg.gate_up_cb if j < 2 else cfg.down_cb)
+            layer.experts.append(lin)
+            words[3 * e + j] = trellis_words_torch(seed, p + ".trellis", i_f, o_f, K, dev)
+    layer.shared = [synth.make_dense_linear(seed, f"{tag}.shared_experts.gate_proj", H, 1024),
+                    synth.make_dense_linear(seed, f"{tag}.shared_experts.up_proj", H, 1024),
+                    synth.make_dense_linear(seed, f"{tag}.shared_experts.down_proj", 1024, H)]
+    return layer, words
+
+
+def oracle_experts(layer, words, used):
+    out = []
+    dummy = dict(trellis=np.zeros(16, np.uint16), suh=np.zeros(1, np.uint16),
+                 svh=np.zeros(1, np.uint16), K=1, cb=0, **{"in": 16, "out": 16})
+    for i, lin in enumerate(layer.experts):
+        if i // 3 in used:
+            d = dict(lin.oracle_dict()) if lin.trellis is not None else None
+            if d is None:
+                d = dict(trellis=words[i].cpu().numpy().view(np.uint16), suh=lin.suh, svh=lin.svh,
+                         K=lin.K, cb=lin.cb, **{"in": lin.in_f, "out": lin.out_f})
+            out.append(d)
+        else:
+            out.append(dummy)
+    return out
+
+
+def test_glm5_layer_b8_vs_oracle(oracle, dev):
+    # GLM-5-shaped layer at batch 8
+    layer, words = glm5_layer_on_device(dev, 31, "glm5")
+    cfg = layer.cfg
+    d = DeviceMoeLayer(layer, dev, words=words)
+    h = synth.activations(31, "glm5.x", 8, cfg.hidden)
+    x = to_dev(h, dev, 8, 1, cfg.hidden)
+    d.diag_enable()
+    y = d(x)
+    _, ids = d.route(x)
+    oc = ocfg_of(oracle, cfg, True)
+    logits = oracle.router_logits(h, layer.router_w)
+    idx, w, flips = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+    used = set(idx.reshape(-1).tolist())
+    want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used),
+                                   [l.oracle_dict() for l in layer.shared], h, idx, w)
+    rel, cos = check_out(y, want)
+    dg = d.diag()
+    assert dg["calls"] == 1 and dg["pairs"] == 64 and dg["distinct_experts"] == len(used)
+    print(f"\nglm5 B=8: distinct experts {len(used)}, max|err|/rms {rel:.3g}, cos {cos:.7f}, "
+          f"near-tie flips {flips}")
+    d.close()
+
+
+def test_glm5_b64_run_grouping(oracle, dev):
+    # 48 of 64 rows identical -> 8 runs of >= 48 rows; 16 independent rows
+    layer, words = glm5_layer_on_device(dev, 41, "glm5b")
+    cfg = layer.cfg
+    d = DeviceMoeLayer(layer, dev, words=words)
+    same = synth.activations(41, "b64.same", 1, cfg.hidden)
+    rest = synth.activations(41, "b64.rest", 16, cfg.hidden)
+    h = np.concatenate([np.repeat(same, 48, 0), rest], 0)
+    x = to_dev(h, dev, 64, 1, cfg.hidden)
+    d.diag_enable()
+    y = d(x)
+    oc = ocfg_of(oracle, cfg, True)
+    logits = oracle.router_logits(h, layer.router_w)
+    _, ids = d.route(x)
+    idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+    runs = oracle.moe_runs(idx)
+    hist = {}
+    for r in runs["run_len"].tolist():
+        hist[min(r, 64)] = hist.get(min(r, 64), 0) + 1
+    dg = d.diag()
+    assert dg["run_hist"] == hist
+    assert sum(1 for r in runs["run_len"] if r >= 48) >= 8
+    used = set(idx.reshape(-1).tolist())
+    want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used),
+                                   [l.oracle_dict() for l in layer.shared], h, idx, w)
+    check_out(y, want)
+    # the 48 identical rows give identical outputs
+    yc = y.view(64, -1).cpu()
+    assert all(torch.equal(yc[i], yc[0]) for i in range(48))
+    d.close()

@@ -1,0 +1,159 @@
+"""GPU parity tests of the trellis tensor path through the C ABI.
+
+Bit-exact against the oracle: decode (W_hat), reconstruct (W), the Hadamard steps.
+Tolerance (stated per test) against the oracle's f64 GEMV: matmul_raw and linear.
+Bit-exact invariants of the reference (tests/glm5_gemv_nt_test.cpp, moe_test.cpp):
+the row-block knob moves no byte, grouped == per-member, rows == single rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+from exl3_amd import synth
+from exl3_amd.trellis import (TrellisWeight, f16_from_bits, trellis_decode, trellis_hadamard,
+                              trellis_linear, trellis_linear_group, trellis_linear_group_rows,
+                              trellis_linear_group_rows_scaled, trellis_matmul_raw,
+                              trellis_pack, trellis_reconstruct, trellis_set_tuning)
+
+pytestmark = pytest.mark.gpu
+SEED = 77
+
+
+def make(dev, in_f, out_f, K, cb, name, scale_std=0.05):
+    words = synth.trellis_words(SEED, name, in_f, out_f, K)
+    su = synth.normal_f16(SEED, name + ".suh", (in_f,), 1.0, scale_std)
+    sv = synth.normal_f16(SEED, name + ".svh", (out_f,), 1.0, scale_std)
+    w = TrellisWeight(trellis_pack(words, in_f // 16, out_f // 16, K, dev),
+                      f16_from_bits(su, dev), f16_from_bits(sv, dev), in_f, out_f, K, cb)
+    return w, words, su, sv
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().cpu().numpy().view(np.uint16)
+
+
+def x_f16(dev, rows, n, name):
+    return torch.from_numpy(synth.activations(SEED, name, rows, n).view(np.float16)).to(dev)
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_decode_bit_exact(oracle, dev, K, cb):
+    # 4096 x 4096 at every K and codebook
+    w, words, _, _ = make(dev, 4096, 4096, K, cb, f"dec.{K}.{cb}")
+    got = bits(trellis_decode(w))
+    want = oracle.decode_inner(words, 4096, 4096, K, cb)
+    assert np.array_equal(got, want)
+
+
+def test_decode_small_and_ragged_shapes(oracle, dev):
+    for (i, o, K, cb) in [(16, 16, 1, 0), (16, 48, 8, 2), (48, 16, 5, 1), (160, 272, 3, 0)]:
+        w, words, _, _ = make(dev, i, o, K, cb, f"decs.{i}.{o}")
+        assert np.array_equal(bits(trellis_decode(w)), oracle.decode_inner(words, i, o, K, cb))
+
+
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_reconstruct_bit_exact(oracle, dev, K):
+    for cb in range(3):
+        w, words, su, sv = make(dev, 512, 640, K, cb, f"rec.{K}.{cb}")
+        got = bits(trellis_reconstruct(w))
+        assert np.array_equal(got, oracle.reconstruct(words, 512, 640, K, cb, su, sv))
+
+
+def test_hadamard_bit_exact(oracle, dev):
+    x = synth.activations(SEED, "had.x", 7, 1024)
+    s = synth.normal_f16(SEED, "had.s", (1024,), 1.0, 0.05)
+    got = bits(trellis_hadamard(torch.from_numpy(x.view(np.float16)).to(dev),
+                                f16_from_bits(s, dev), pre=True))
+    assert np.array_equal(got, oracle.had_pre(x, s))
+    y = synth.normal_f32(SEED, "had.y", (7, 1024), 0.0, 30.0)
+    got = bits(trellis_hadamard(torch.from_numpy(y).to(dev), f16_from_bits(s, dev), pre=False))
+    assert np.array_equal(got, oracle.had_post(y, s))
+    # stacked: 3 members x 2 rows, one scale vector per member
+    st = synth.normal_f16(SEED, "had.st", (3, 1024), 1.0, 0.05)
+    x6 = synth.activations(SEED, "had.x6", 6, 1024)
+    got = bits(trellis_hadamard(torch.from_numpy(x6.view(np.float16)).to(dev),
+                                f16_from_bits(st, dev), pre=True, stacked=3))
+    for m in range(3):
+        assert np.array_equal(got[2 * m:2 * m + 2], oracle.had_pre(x6[2 * m:2 * m + 2], st[m]))
+
+
+def gemv_bound(xhat_bits, what_bits):
+    """Per-output bound for f32 accumulation against the f64 sum: 64 f32 ulps of
+    sum_k |x_k w_kn| (a wrong decode or layout is off by O(|w| |x|) ~ 1)."""
+    x = np.abs(xhat_bits.view(np.float16).astype(np.float64))
+    w = np.abs(what_bits.view(np.float16).astype(np.float64))
+    return 64 * 2.0 ** -24 * (x @ w)
+
+
+@pytest.mark.parametrize("K,cb", [(1, 2), (2, 0), (3, 1), (4, 1), (5, 1), (6, 0), (8, 2)])
+def test_matmul_raw_vs_f64(oracle, dev, K, cb):
+    in_f, out_f, rows = 4096, 1024, 3
+    w, words, _, _ = make(dev, in_f, out_f, K, cb, f"mm.{K}.{cb}")
+    xh = synth.normal_f16(SEED, f"mm.x.{K}", (rows, in_f), 0.0, 1.0)
+    got = trellis_matmul_raw(w, torch.from_numpy(xh.view(np.float16)).to(dev)).cpu().numpy()
+    want = oracle.matmul_raw(words, in_f, out_f, K, cb, xh)
+    bound = gemv_bound(xh, oracle.decode_inner(words, in_f, out_f, K, cb))
+    assert np.all(np.abs(got - want) <= bound)
+
+
+# f16 output tolerance of one linear: the f32-vs-f64 GEMV difference can move the f16
+# rounding of yhat by one ulp before the output Hadamard mixes 128 of them.
+LIN_TOL_RMS = 2e-3
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_linear_sweep_4096(oracle, dev, K, cb):
+    # in = out = 4096, rows = 1
+    w, words, su, sv = make(dev, 4096, 4096, K, cb, f"lin.{K}.{cb}")
+    x = synth.activations(SEED, f"lin.x.{K}.{cb}", 1, 4096)
+    got = bits(trellis_linear(w, torch.from_numpy(x.view(np.float16)).to(dev)))
+    want = oracle.trellis_linear(words, 4096, 4096, K, cb, su, sv, x)
+    g = got.view(np.float16).astype(np.float64)
+    r = want.view(np.float16).astype(np.float64)
+    rms = np.sqrt(np.mean(r ** 2))
+    assert np.isfinite(g).all() and rms > 0.1
+    assert np.max(np.abs(g - r)) <= LIN_TOL_RMS * rms
+    assert np.mean(got == want) > 0.9
+
+
+def test_rows_invariance_and_row_block_knob(dev):
+    w, *_ = make(dev, 2048, 1024, 3, 2, "inv")
+    x = x_f16(dev, 13, 2048, "inv.x")
+    base = bits(trellis_linear(w, x))
+    for r in range(13):
+        assert np.array_equal(bits(trellis_linear(w, x[r:r + 1].contiguous())), base[r:r + 1])
+    try:
+        for mb in (1, 2, 4):
+            trellis_set_tuning(rows_per_pass=mb)
+            assert np.array_equal(bits(trellis_linear(w, x)), base)
+    finally:
+        trellis_set_tuning()
+
+
+def test_grouped_equals_members(dev):
+    ws = [make(dev, 1024, 512, 4, 1, f"grp.{i}")[0] for i in range(5)]
+    x = x_f16(dev, 2, 1024, "grp.x")
+    g = bits(trellis_linear_group(ws, x))
+    for i, w in enumerate(ws):
+        assert np.array_equal(g[i], bits(trellis_linear(w, x)))
+    xr = x_f16(dev, 5 * 3, 1024, "grp.xr").view(5, 3, 1024)
+    gr = bits(trellis_linear_group_rows(ws, xr, 3))
+    for i, w in enumerate(ws):
+        assert np.array_equal(gr[i], bits(trellis_linear(w, xr[i].contiguous())))
+    # scale-stack form with the members' own scales is bit-identical
+    suh = torch.stack([w.suh for w in ws])
+    svh = torch.stack([w.svh for w in ws])
+    gs = bits(trellis_linear_group_rows_scaled(ws, xr, 3, suh, svh))
+    assert np.array_equal(gs, gr)
+
+
+def test_many_members_beyond_one_launch(dev):
+    # more members than one kernel-argument table holds: chunked launches, same bytes
+    w, words, su, sv = make(dev, 128, 128, 2, 0, "many")
+    ws = [w] * 130
+    x = x_f16(dev, 1, 128, "many.x")
+    g = bits(trellis_linear_group(ws, x))
+    one = bits(trellis_linear(w, x))
+    assert all(np.array_equal(g[i], one) for i in range(130))
