@@ -160,7 +160,7 @@ def main():
     for i in range(args.layers * 8):
         step(i)
     torch.cuda.synchronize()
-    tm = {k: 0.0 for k in ("calls", "router_ms", "shared_ms", "gate_up_ms", "down_ms", "total_ms",
+    tm = {k: 0.0 for k in ("calls", "router_ms", "gate_up_ms", "down_ms", "combine_ms", "total_ms",
                            "gate_up_trellis_bytes", "down_trellis_bytes")}
     for _, _, d in layers:
         d.timing_enable(False)
@@ -202,8 +202,8 @@ def main():
                           "algorithmic_bytes_per_launch": round(dn_bytes), "avg_launch_ms": round(dn_ms, 5)},
         "routed_trellis_GBps": round(routed_gbps, 1),
         "distinct_experts_per_step": round(distinct, 2),
-        "stages_ms": {k: round(tm[k] / calls, 5) for k in ("router_ms", "shared_ms", "gate_up_ms",
-                                                           "down_ms", "total_ms")},
+        "stages_ms": {k: round(tm[k] / calls, 5) for k in ("router_ms", "gate_up_ms", "down_ms",
+                                                           "combine_ms", "total_ms")},
         "gpu_ms_per_step_events": round(gpu_ms / args.steps, 5),
     }
     if not args.no_cpu_baseline:

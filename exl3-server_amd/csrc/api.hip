@@ -55,7 +55,7 @@ using namespace exl3h;
 namespace {
 
 // Workspace carve-up for the single/grouped linear: xhat f16 (n, rows, in) then the
-// split partials f32 (n, S, rows, out).
+// chunk partials f32 (n, n_chunks, rows, out).
 struct LinearWs {
   size_t xhat_off, part_off, total;
 };
@@ -65,7 +65,7 @@ LinearWs linear_ws(int in, int out, int64_t rows, int n) {
   LinearWs w;
   w.xhat_off = 0;
   w.part_off = align_up((size_t)n * rows * in * 2, 256);
-  w.total = w.part_off + align_up((size_t)n * kp.S * rows * out * 4, 256);
+  w.total = w.part_off + align_up((size_t)n * kp.n_chunks * rows * out * 4, 256);
   return w;
 }
 
@@ -122,7 +122,7 @@ exl3_status linear_core(const exl3_trellis_desc *members, int n, const uint16_t 
     }
     rc = launch_qmv(w0, tr, cn, xh, x_stride, rows, part, st);
     if (rc) return rc;
-    rc = launch_qmv_finalize(cn, kp.S, rows, out, part,
+    rc = launch_qmv_finalize(cn, kp.n_chunks, rows, out, part,
                              y32 ? y32 + (int64_t)c0 * rows * out : nullptr,
                              y16 ? y16 + (int64_t)c0 * rows * out : nullptr, sv, st);
     if (rc) return rc;
@@ -164,7 +164,7 @@ exl3_status exl3_trellis_path_info(const exl3_trellis_desc *w, int64_t rows,
   info->rows_per_block = mb;
   info->pad_rows = (int32_t)((rows + mb - 1) / mb * mb);
   info->passes = (int32_t)((rows + mb - 1) / mb);
-  info->splits = kp.S;
+  info->splits = kp.n_chunks;
   info->tiles_per_workgroup = 8;
   return EXL3_OK;
 }

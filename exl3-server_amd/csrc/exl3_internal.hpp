@@ -31,27 +31,17 @@ inline hipStream_t stream_of(exl3_stream_t s) { return reinterpret_cast<hipStrea
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// The k partition of a trellis GEMV, a function of the tensor shape only (so every
-// entry point that sees a shape sums it in the same f32 order):
-//   waves per workgroup  kWaves (fixed)
-//   k-tiles per wave     T
-//   k-splits             S = k_tiles / (kWaves * T), summed in split order
-// Each output element is ((w0 + w1) + w2) + w3 over the workgroup's waves, then
-// s0 + s1 + ... over splits; inside a wave the k-tiles are visited in order.
-constexpr int kWaves = 4;
-
+// The k partition of a trellis GEMV, a function of the tensor's k-tile count only: the
+// k range is cut into chunks of `ct` k-tiles, each summed from zero by one wave, and
+// an output is the in-order sum of its chunk partials (device side: qmv_core.hpp).
 struct KPart {
-  int T;
-  int S;
+  int ct;        // k-tiles per chunk
+  int n_chunks;  // chunks per output column
 };
 
 inline KPart kpart(int k_tiles) {
-  int T;
-  if (k_tiles >= 256 && k_tiles % 64 == 0) T = 16;
-  else if (k_tiles % 32 == 0) T = 8;
-  else if (k_tiles % 16 == 0) T = 4;
-  else T = 2;
-  return KPart{T, k_tiles / (kWaves * T)};
+  const int ct = (k_tiles % 16 == 0) ? 16 : 8;
+  return KPart{ct, k_tiles / ct};
 }
 
 // Scheduling knobs (exl3_set_tuning).
@@ -76,13 +66,13 @@ exl3_status launch_hadamard(const uint16_t *x16, const float *x32, int64_t rows,
                             hipStream_t st);
 
 // xhat: (n, rows, in) f16 (member stride rows*in, or 0 when shared); part: f32
-// (n, S, rows, out).
+// (n, n_chunks, rows, out).
 exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, int n,
                        const uint16_t *xhat, int64_t x_member_stride, int64_t rows, float *part,
                        hipStream_t st);
-// Sums the S partials in split order into y32 (raw f32, (n, rows, out)) or, through
+// Sums the chunk partials in chunk order into y32 (raw f32, (n, rows, out)) or, through
 // the output Hadamard with member m's svh.p[m], into y16 (n, rows, out).
-exl3_status launch_qmv_finalize(int n, int S, int64_t rows, int out, const float *part,
+exl3_status launch_qmv_finalize(int n, int n_chunks, int64_t rows, int out, const float *part,
                                 float *y32, uint16_t *y16, const PtrTable &svh,
                                 hipStream_t st);
 

@@ -14,6 +14,7 @@
 #include "exl3_internal.hpp"
 #include "exl3_moe.h"
 #include "moe_common.hpp"
+#include "moe_dense.hpp"
 
 using namespace exl3d;
 using exl3m::ExpertTab;
@@ -21,7 +22,7 @@ using exl3m::MoeArgs;
 
 namespace exl3h {
 exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const MoeArgs &a,
-                              int shared_mode, hipStream_t st);
+                              int shared_mode, int routed_blocks, hipStream_t st);
 }
 
 namespace {
@@ -31,47 +32,29 @@ __device__ __forceinline__ float hi16(uint32_t v) { return (float)bitcast<f16>((
 __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 
 // ---------------------------------------------------------------------------------
-// Router logits: logits[t][e] = sum_k f32(h[t][k]) * f32(router_w[e][k])
-// (glm5_moe.cpp:127-128). One wave per expert, 8 token rows per workgroup; f16*f16
-// products are exact in f32. Also clears the layer's completion counters.
+// L1. Router logits: logits[t][e] = sum_k f32(h[t][k]) * f32(router_w[e][k])
+// (glm5_moe.cpp:127-128): one wave per expert, 8 token rows per workgroup staged in
+// LDS; f16*f16 products are exact in f32. Workgroups past the logits compute the f16
+// shared expert's gate/up k-split partials (one per projection, 128-column block and
+// 256-row k split).
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_moe_logits(MoeArgs a) {
-  const int lin = blockIdx.y * gridDim.x + blockIdx.x;
-  for (int i = lin * 256 + threadIdx.x; i < a.n_counters; i += gridDim.x * gridDim.y * 256) {
-    if (i < a.n_counters) a.gu_cnt[i] = 0;  // gu_cnt, dn_cnt, comb_cnt are contiguous
+__global__ __launch_bounds__(256) void k_moe_pre(MoeArgs a) {
+  extern __shared__ uint32_t pre_lds[];
+  if ((int)blockIdx.x >= a.n_logit_blocks) {
+    const int b = blockIdx.x - a.n_logit_blocks;
+    const int n_cb = a.SI / 128, S = dense_splits(a.H);
+    const int proj = b / (n_cb * S), rem = b % (n_cb * S);
+    dense_skinny(a.h, a.N, a.H, a.SI, a.sh_dense[proj], a.dsh_gu + (int64_t)proj * S * a.N * a.SI,
+                 rem % n_cb, rem / n_cb, pre_lds);
+    return;
   }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int e = blockIdx.x * 4 + wave;
-  if (e >= a.E) return;
-  const int r0 = blockIdx.y * 8;
-  const int nr = min(8, a.N - r0);
-  float acc[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
-  const uint16_t *wrow = a.router_w + (int64_t)e * a.H;
-  for (int k = lane * 8; k < a.H; k += 512) {
-    const uint4 w4 = *reinterpret_cast<const uint4 *>(wrow + k);
-    const uint32_t wv[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      if (r >= nr) break;
-      const uint4 x4 = *reinterpret_cast<const uint4 *>(a.h + (int64_t)(r0 + r) * a.H + k);
-      const uint32_t xv[4] = {x4.x, x4.y, x4.z, x4.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc[r] = fmaf(lo16(xv[q]), lo16(wv[q]), acc[r]);
-        acc[r] = fmaf(hi16(xv[q]), hi16(wv[q]), acc[r]);
-      }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    float v = acc[r];
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    if (lane == 0 && r < nr) a.logits[(int64_t)(r0 + r) * a.E + e] = v;
-  }
+  const int eb = (a.E + 3) / 4;
+  router_logits(a.h, a.N, a.H, a.router_w, a.E, a.logits, (blockIdx.x % eb) * 4,
+                (int64_t)(blockIdx.x / eb) * 8, pre_lds);
 }
+
+// LDS bytes of k_moe_pre: the logits' 8 staged rows, or a dense_skinny workgroup.
+size_t pre_lds_bytes(int H) { return std::max<size_t>(16 * (size_t)H, 4 * (size_t)kDenseLdsWords); }
 
 // ---------------------------------------------------------------------------------
 // Routing + dispatch, one workgroup of 16 waves (glm5_moe.cpp:16-60, 158-255).
@@ -99,10 +82,37 @@ __device__ __forceinline__ uint64_t lanes_below() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+__device__ __forceinline__ float swiglu1(float g, float u, float L) {
+  if (L > 0.0f) {
+    g = fminf(g, L);
+    u = fminf(fmaxf(u, -L), L);
+  }
+  const float sg = rf16(1.0f / (1.0f + expf(-g)));
+  const float act = rf16(g * sg);
+  return rf16(act * u);
+}
+
+// L2. Workgroup 0: routing + dispatch. Workgroups 1..: the f16 shared expert's SwiGLU
+// on its gate/up partials (summed in split order, rounded to f16 like the matmul).
 __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int32_t *id_out,
                                                     int do_dispatch) {
   __shared__ float s_buf[16][kMaxE];  // group path: scores_for_choice per wave; dispatch: counts
   __shared__ int s_keep[16][64];
+  if (blockIdx.x > 0) {
+    const int64_t i = (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x;
+    const int64_t n = (int64_t)a.N * a.SI;
+    if (i >= n) return;
+    const int S = dense_splits(a.H);
+    const float *pg = a.dsh_gu, *pu = a.dsh_gu + (int64_t)S * n;
+    float g = pg[i], u = pu[i];
+    for (int s = 1; s < S; ++s) {
+      g += pg[(int64_t)s * n + i];
+      u += pu[(int64_t)s * n + i];
+    }
+    const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
+    a.dsh_act[i] = bitcast<uint16_t>(to_f16(swiglu1(rf16(g), rf16(u), L)));
+    return;
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = a.E, K = a.topk;
   const int ng = a.n_group > 1 ? a.n_group : 1;
@@ -300,84 +310,45 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
 }
 
 // ---------------------------------------------------------------------------------
-// Dense f16 shared expert (g5_linear's mx::matmul branch, glm5_kda.cpp:120):
-// part[s][row][n] = sum over k in [128 s, 128 s + 128) of x[row][k] * W[k][n].
+// L5. Combine (glm5_moe.cpp:411-416): one wave per (token row, 128-column block):
+// routed = f16(sum over ranks, in rank order, of the slots' f16(y * w)), then
+// out = f16(routed + shared).
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_dense_part(const uint16_t *__restrict__ x, int64_t rows,
-                                                    int in, int out,
-                                                    const uint16_t *__restrict__ W,
-                                                    float *__restrict__ part) {
-  __shared__ uint32_t xs[16][64];
-  const int n = blockIdx.x * 512 + 2 * threadIdx.x;
-  const int s = blockIdx.y, k0 = s * 128;
-  for (int64_t r0 = 0; r0 < rows; r0 += 16) {
-    const int nr = (int)min<int64_t>(16, rows - r0);
-    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
-      const int r = i >> 6, wd = i & 63;
-      xs[r][wd] = r < nr ? reinterpret_cast<const uint32_t *>(x + (r0 + r) * in + k0)[wd] : 0u;
+__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int n_cb = a.H / 128;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gw >= (int64_t)a.N * n_cb) return;
+  const int row = (int)(gw / n_cb), cb = (int)(gw % n_cb);
+  const int c = cb * 128 + 2 * lane;
+  float r0 = 0.0f, r1 = 0.0f;
+  for (int k = 0; k < a.topk; ++k) {
+    const int sl = a.slot[(int64_t)row * a.topk + k];
+    const uint32_t v = *reinterpret_cast<const uint32_t *>(a.yw + (int64_t)sl * a.H + c);
+    r0 += lo16(v);
+    r1 += hi16(v);
+  }
+  r0 = rf16(r0);
+  r1 = rf16(r1);
+  if (a.shared_kind == exl3m::kSharedTrellis) {
+    const uint32_t sv = *reinterpret_cast<const uint32_t *>(a.sh_out + (int64_t)row * a.H + c);
+    r0 += lo16(sv);
+    r1 += hi16(sv);
+  } else if (a.shared_kind == exl3m::kSharedDense) {
+    const int S = dense_splits(a.SI);
+    const int64_t n = (int64_t)a.N * a.H;
+    const float *p = a.dsh_dn + (int64_t)row * a.H + c;
+    float s0 = p[0], s1 = p[1];
+    for (int s = 1; s < S; ++s) {
+      s0 += p[(int64_t)s * n];
+      s1 += p[(int64_t)s * n + 1];
     }
-    __syncthreads();
-    float acc[16][2];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r][0] = acc[r][1] = 0.0f;
-    if (n < out) {
-      for (int k = 0; k < 128; k += 2) {
-        const uint32_t w0 = *reinterpret_cast<const uint32_t *>(W + (int64_t)(k0 + k) * out + n);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t *>(W + (int64_t)(k0 + k + 1) * out + n);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint32_t xv = xs[r][k >> 1];
-          acc[r][0] = fmaf(lo16(xv), lo16(w0), acc[r][0]);
-          acc[r][1] = fmaf(lo16(xv), hi16(w0), acc[r][1]);
-          acc[r][0] = fmaf(hi16(xv), lo16(w1), acc[r][0]);
-          acc[r][1] = fmaf(hi16(xv), hi16(w1), acc[r][1]);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if (r >= nr) break;
-        float *p = part + ((int64_t)s * rows + r0 + r) * out + n;
-        p[0] = acc[r][0];
-        p[1] = acc[r][1];
-      }
-    }
-    __syncthreads();
+    r0 += rf16(s0);
+    r1 += rf16(s1);
   }
-}
-
-__device__ __forceinline__ float swiglu1(float g, float u, float L) {
-  if (L > 0.0f) {
-    g = fminf(g, L);
-    u = fminf(fmaxf(u, -L), L);
-  }
-  const float sg = rf16(1.0f / (1.0f + expf(-g)));
-  const float act = rf16(g * sg);
-  return rf16(act * u);
-}
-
-// act[row][c] = swiglu(f16(sum_s gate part), f16(sum_s up part))
-__global__ __launch_bounds__(256) void k_dense_swiglu(const float *__restrict__ pg,
-                                                      const float *__restrict__ pu, int S,
-                                                      int64_t rows, int n, float limit,
-                                                      uint16_t *__restrict__ act) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= rows * n) return;
-  float g = pg[i], u = pu[i];
-  for (int s = 1; s < S; ++s) {
-    g += pg[(int64_t)s * rows * n + i];
-    u += pu[(int64_t)s * rows * n + i];
-  }
-  const float L = limit > 0.0f ? rf16(limit) : 0.0f;
-  act[i] = bitcast<uint16_t>(to_f16(swiglu1(rf16(g), rf16(u), L)));
-}
-
-__global__ __launch_bounds__(256) void k_dense_out(const float *__restrict__ p, int S, int64_t count,
-                                                   uint16_t *__restrict__ y) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= count) return;
-  float v = p[i];
-  for (int s = 1; s < S; ++s) v += p[(int64_t)s * count + i];
-  y[i] = bitcast<uint16_t>(to_f16(v));
+  const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(r0)) |
+                     ((uint32_t)bitcast<uint16_t>(to_f16(r1)) << 16);
+  *reinterpret_cast<uint32_t *>(a.out + (int64_t)row * a.H + c) = o;
 }
 
 }  // namespace
@@ -391,7 +362,7 @@ struct exl3_moe_layer_s {
   exl3_moe_config cfg;
   int H, I, E, topk;
   int gu_K, gu_cb, dn_K, dn_cb;
-  int shared;        // 0 none, 1 trellis, 2 dense
+  int shared;        // exl3m::SharedKind
   int SI, sh_K, sh_cb, sh_dn_K, sh_dn_cb;
   const uint16_t *sh_dense[3];
   const uint16_t *router_w;
@@ -413,9 +384,8 @@ namespace {
 struct MoeLayout {
   size_t total;
   size_t logits, weights, ids, sorted_row, sorted_rank, slot, run_expert, run_off, run_len, n_runs;
-  size_t gu_part, act_hat, dn_part, yw, sh_out, counters, dsh_part, dsh_act;
-  int P, R, Imax, Sgu, Sdn, cnt_stride, n_counters;
-  int64_t dsh_part_elems;
+  size_t yhat_gu, yw, sh_out, dsh_gu, dsh_act, dsh_dn;
+  int P, R, Imax;
 };
 
 MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
@@ -424,10 +394,6 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.P = (int)(N * K);
   m.R = std::min<int64_t>(E, m.P);
   m.Imax = std::max(I, SI);
-  m.Sgu = kpart(H / 16).S;
-  m.Sdn = std::max(kpart(I / 16).S, SI ? kpart(SI / 16).S : 1);
-  m.cnt_stride = std::max(m.Imax / 128, H / 128);
-  m.n_counters = (int)(2 * (int64_t)(m.R + 1) * m.cnt_stride + N * (H / 128));
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -435,6 +401,7 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
     return at;
   };
   const int64_t slots = m.P + N;
+  const bool dense = L->shared == exl3m::kSharedDense;
   m.logits = take(4 * N * E);
   m.weights = take(4 * (size_t)m.P);
   m.ids = take(4 * (size_t)m.P);
@@ -445,18 +412,12 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.run_off = take(4 * (size_t)m.R);
   m.run_len = take(4 * (size_t)m.R);
   m.n_runs = take(4);
-  m.gu_part = take(4 * (size_t)slots * 2 * m.Sgu * m.Imax);
-  m.act_hat = take(2 * (size_t)slots * m.Imax);
-  m.dn_part = take(4 * (size_t)slots * m.Sdn * H);
+  m.yhat_gu = take(4 * (size_t)slots * 2 * m.Imax);
   m.yw = take(2 * (size_t)m.P * H);
   m.sh_out = take(2 * (size_t)N * H);
-  m.counters = take(4 * (size_t)m.n_counters);
-  m.dsh_part_elems = 0;
-  if (L->shared == 2) {
-    m.dsh_part_elems = std::max<int64_t>(2 * (int64_t)(H / 128) * N * SI, (int64_t)(SI / 128) * N * H);
-  }
-  m.dsh_part = take(4 * (size_t)m.dsh_part_elems);
-  m.dsh_act = take(2 * (size_t)N * (L->shared == 2 ? SI : 0));
+  m.dsh_gu = take(dense ? 4 * (size_t)2 * dense_splits(H) * N * SI : 0);
+  m.dsh_act = take(dense ? 2 * (size_t)N * SI : 0);
+  m.dsh_dn = take(dense ? 4 * (size_t)dense_splits(SI) * N * H : 0);
   m.total = o;
   return m;
 }
@@ -478,14 +439,13 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.norm_topk_prob = L->cfg.norm_topk_prob;
   a.routed_scaling_factor = L->cfg.routed_scaling_factor;
   a.swiglu_limit = L->cfg.swiglu_limit;
-  a.has_shared = L->shared ? 1 : 0;
-  a.Sgu = m.Sgu;
-  a.Sdn = m.Sdn;
-  a.cnt_stride = m.cnt_stride;
+  a.shared_kind = L->shared;
+  a.n_logit_blocks = (int)(((a.E + 3) / 4) * ((N + 7) / 8));
   a.h = h;
   a.router_w = L->router_w;
   a.router_bias = L->router_bias;
   a.tab = L->tab_dev;
+  for (int j = 0; j < 3; ++j) a.sh_dense[j] = L->sh_dense[j];
   a.logits = (float *)(ws + m.logits);
   a.weights = (float *)(ws + m.weights);
   a.ids = (int32_t *)(ws + m.ids);
@@ -496,17 +456,12 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.run_off = (int32_t *)(ws + m.run_off);
   a.run_len = (int32_t *)(ws + m.run_len);
   a.n_runs = (int32_t *)(ws + m.n_runs);
-  a.gu_part = (float *)(ws + m.gu_part);
-  a.act_hat = (uint16_t *)(ws + m.act_hat);
-  a.dn_part = (float *)(ws + m.dn_part);
+  a.yhat_gu = (float *)(ws + m.yhat_gu);
   a.yw = (uint16_t *)(ws + m.yw);
   a.sh_out = (uint16_t *)(ws + m.sh_out);
-  a.gu_cnt = (uint32_t *)(ws + m.counters);
-  a.dn_cnt = a.gu_cnt + (int64_t)(m.R + 1) * m.cnt_stride;
-  a.comb_cnt = a.dn_cnt + (int64_t)(m.R + 1) * m.cnt_stride;
-  a.n_counters = m.n_counters;
-  a.dsh_part = (float *)(ws + m.dsh_part);
+  a.dsh_gu = (float *)(ws + m.dsh_gu);
   a.dsh_act = (uint16_t *)(ws + m.dsh_act);
+  a.dsh_dn = (float *)(ws + m.dsh_dn);
   a.out = out;
   return a;
 }
@@ -522,14 +477,24 @@ exl3_status check_linear(const exl3_linear_desc &d, int in, int out, const char 
   return EXL3_OK;
 }
 
+// L1 + L2: logits (+ f16 shared gate/up partials), then routing/dispatch (+ f16
+// shared SwiGLU). w_out / id_out receive the routing.
 exl3_status launch_logits_route(exl3_moe_layer_s *L, const MoeArgs &a, float *w_out, int32_t *id_out,
                                 int do_dispatch, hipStream_t st) {
-  dim3 g1((unsigned)((a.E + 3) / 4), (unsigned)((a.N + 7) / 8));
-  k_moe_logits<<<g1, 256, 0, st>>>(a);
-  EXL3_LAUNCHED("k_moe_logits");
-  k_moe_route<<<1, 1024, 0, st>>>(a, w_out, id_out, do_dispatch);
+  const bool dense = do_dispatch && L->shared == exl3m::kSharedDense;
+  int pre_blocks = a.n_logit_blocks;
+  if (dense) pre_blocks += 2 * (a.SI / 128) * dense_splits(a.H);
+  const size_t lds = pre_lds_bytes(a.H);
+  static std::once_flag attr_once;
+  std::call_once(attr_once, [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_moe_pre),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  });
+  k_moe_pre<<<pre_blocks, 256, lds, st>>>(a);
+  EXL3_LAUNCHED("k_moe_pre");
+  const int fin_blocks = dense ? (int)(((int64_t)a.N * a.SI + 1023) / 1024) : 0;
+  k_moe_route<<<1 + fin_blocks, 1024, 0, st>>>(a, w_out, id_out, do_dispatch);
   EXL3_LAUNCHED("k_moe_route");
-  (void)L;
   return EXL3_OK;
 }
 
@@ -554,6 +519,7 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
   const int K = cfg->num_experts_per_tok;
   if (H <= 0 || H % 128 || I <= 0 || I % 128)
     return fail(EXL3_ERR_INVALID, "hidden and intermediate sizes must be positive multiples of 128");
+  if (H > 8192) return fail(EXL3_ERR_UNSUPPORTED, "hidden_size must be <= 8192");
   if (E <= 0 || E > 1024) return fail(EXL3_ERR_UNSUPPORTED, "n_routed_experts must be in 1..1024");
   if (K <= 0 || K > E || K > 64) return fail(EXL3_ERR_INVALID, "num_experts_per_tok must be in 1..min(E, 64)");
   const int ng = cfg->n_group > 1 ? cfg->n_group : 1;
@@ -746,40 +712,29 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[1], st));
 
-  const int H = layer->H;
-  if (layer->shared == 2) {
-    const int SI = layer->SI;
-    const int S1 = H / 128, S2 = SI / 128;
-    float *pg = a.dsh_part, *pu = a.dsh_part + (int64_t)S1 * N * SI;
-    k_dense_part<<<dim3((SI + 511) / 512, S1), 256, 0, st>>>(h, N, H, SI, layer->sh_dense[0], pg);
-    k_dense_part<<<dim3((SI + 511) / 512, S1), 256, 0, st>>>(h, N, H, SI, layer->sh_dense[1], pu);
-    EXL3_LAUNCHED("k_dense_part");
-    k_dense_swiglu<<<(unsigned)((N * SI + 255) / 256), 256, 0, st>>>(pg, pu, S1, N, SI,
-                                                                     layer->cfg.swiglu_limit, a.dsh_act);
-    EXL3_LAUNCHED("k_dense_swiglu");
-    k_dense_part<<<dim3((H + 511) / 512, S2), 256, 0, st>>>(a.dsh_act, N, SI, H, layer->sh_dense[2],
-                                                            a.dsh_part);
-    EXL3_LAUNCHED("k_dense_part");
-    k_dense_out<<<(unsigned)((N * H + 255) / 256), 256, 0, st>>>(a.dsh_part, S2, N * H, a.sh_out);
-    EXL3_LAUNCHED("k_dense_out");
-  } else if (layer->shared == 1) {
-    const int SI = layer->SI;
-    const unsigned gu_blocks = (unsigned)(2 * (SI / 128) * kpart(H / 16).S);
-    rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, gu_blocks, a, 1, st);
-    if (rc) return rc;
-    const unsigned dn_blocks = (unsigned)((H / 128) * kpart(SI / 16).S);
-    rc = launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, dn_blocks, a, 1, st);
-    if (rc) return rc;
-  }
+  const int H = layer->H, I = layer->I, SI = layer->SI;
+  // L3: routed gate/up (+ the f16 shared expert's down partials)
+  const unsigned gu_routed = (unsigned)((int64_t)m.R * 2 * (I / 128));
+  unsigned gu_blocks = gu_routed;
+  if (layer->shared == exl3m::kSharedDense) gu_blocks += (unsigned)((H / 128) * dense_splits(SI));
+  rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, gu_blocks, a, 0, (int)gu_routed, st);
+  if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[2], st));
-  const int I = layer->I;
-  const unsigned gu_blocks = (unsigned)((int64_t)m.R * 2 * (I / 128) * kpart(H / 16).S);
-  rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, gu_blocks, a, 0, st);
+  // L4: routed down
+  rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb, (unsigned)((int64_t)m.R * (H / 128)), a, 0,
+                         0, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[3], st));
-  const unsigned dn_blocks = (unsigned)((int64_t)m.R * (H / 128) * kpart(I / 16).S);
-  rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb, dn_blocks, a, 0, st);
-  if (rc) return rc;
+  // a trellis shared expert: one run of every token row through the same kernels
+  if (layer->shared == exl3m::kSharedTrellis) {
+    rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, (unsigned)(2 * (SI / 128)), a, 1, 0, st);
+    if (rc) return rc;
+    rc = launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, (unsigned)(H / 128), a, 1, 0, st);
+    if (rc) return rc;
+  }
+  // L5: combine
+  k_moe_combine<<<(unsigned)((N * (H / 128) + 3) / 4), 256, 0, st>>>(a);
+  EXL3_LAUNCHED("k_moe_combine");
   if (timed) {
     EXL3_HIP(hipEventRecord(layer->ev[4], st));
     EXL3_HIP(hipEventSynchronize(layer->ev[4]));
@@ -793,9 +748,9 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
     exl3_moe_timing &t = layer->timing;
     t.calls += 1;
     t.router_ms += ms[0];
-    t.shared_ms += ms[1];
-    t.gate_up_ms += ms[2];
-    t.down_ms += ms[3];
+    t.gate_up_ms += ms[1];
+    t.down_ms += ms[2];
+    t.combine_ms += ms[3];
     t.total_ms += ms[0] + ms[1] + ms[2] + ms[3];
     for (int i = 0; i < nr; ++i) {
       t.gate_up_trellis_bytes += layer->gu_bytes[re[i]];

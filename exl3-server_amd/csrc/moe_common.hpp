@@ -1,4 +1,19 @@
 // Shared host/device description of one MoE layer call.
+//
+// A decode call is five stream-ordered launches; every cross-workgroup dependency is
+// a launch boundary (no device-scope fences or completion counters):
+//   L1 k_moe_pre       router logits (+ the f16 shared expert's gate/up partials)
+//   L2 k_moe_route     top-k routing, expert-order dispatch, run table
+//                      (+ the f16 shared expert's SwiGLU)
+//   L3 k_moe_gate_up   routed gate/up, one workgroup per (run, projection, 128-column
+//                      block), full k range; raw f32 outputs per slot
+//                      (+ the f16 shared expert's down partials)
+//   L4 k_moe_down      routed down, one workgroup per (run, 128-column block): SwiGLU
+//                      and the down input Hadamard in its prologue, output Hadamard and
+//                      the routing weight in its epilogue
+//   L5 k_moe_combine   per token row: the top_k terms in rank order + shared expert
+// A trellis shared expert runs the gate/up and down kernels on one extra "run" that
+// holds every token row (two more launches).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -15,6 +30,8 @@ struct ExpertTab {
   const uint16_t *svh[3];
 };
 
+enum SharedKind { kSharedNone = 0, kSharedTrellis = 1, kSharedDense = 2 };
+
 // Everything a kernel of one layer call needs, passed by value.
 struct MoeArgs {
   // shape / config
@@ -26,14 +43,14 @@ struct MoeArgs {
   int E, topk, P, R;  // experts, top-k, pairs N*topk, run-table capacity min(E, P)
   int n_group, topk_group, norm_topk_prob;
   float routed_scaling_factor, swiglu_limit;
-  int has_shared;
-  int Sgu, Sdn;       // k-split counts of the gate/up and down partial planes (strides)
-  int cnt_stride;     // counters per run
+  int shared_kind;    // SharedKind
+  int n_logit_blocks; // L1 workgroups computing router logits
   // inputs
   const uint16_t *h;          // (N, H) f16
   const uint16_t *router_w;   // (E, H) f16
   const float *router_bias;   // (E) f32
   const ExpertTab *tab;       // E (+1) entries
+  const uint16_t *sh_dense[3];  // f16 shared expert weights (in, out) when dense
   // workspace
   float *logits;       // (N, E)
   float *weights;      // (N, topk)
@@ -43,17 +60,12 @@ struct MoeArgs {
   int32_t *slot;         // (P): pair b*topk + k -> slot
   int32_t *run_expert, *run_off, *run_len;  // (R)
   int32_t *n_runs;       // (1)
-  float *gu_part;      // (P + N, 2, Sgu, Imax)
-  uint16_t *act_hat;   // (P + N, Imax): rotated SwiGLU output = the down input xhat
-  float *dn_part;      // (P + N, Sdn, H)
+  float *yhat_gu;      // (P + N, 2, Imax): gate/up outputs before the output Hadamard
   uint16_t *yw;        // (P, H): f16(y * w) per slot
-  uint16_t *sh_out;    // (N, H): shared expert output
-  uint32_t *gu_cnt;    // (R + 1, cnt_stride)
-  uint32_t *dn_cnt;    // (R + 1, cnt_stride)
-  uint32_t *comb_cnt;  // (N, H / 128)
-  int n_counters;      // total counter words (zeroed by the logits kernel)
-  float *dsh_part;     // dense shared expert partials
-  uint16_t *dsh_act;   // (N, SI) dense shared SwiGLU output
+  uint16_t *sh_out;    // (N, H): trellis shared expert output
+  float *dsh_gu;       // (2, H/128, N, SI): f16 shared gate/up k-split partials
+  uint16_t *dsh_act;   // (N, SI): f16 shared expert SwiGLU output
+  float *dsh_dn;       // (SI/128, N, H): f16 shared down k-split partials
   uint16_t *out;       // (N, H)
 };
 

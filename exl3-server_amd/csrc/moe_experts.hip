@@ -1,40 +1,37 @@
 // Routed (and trellis shared) expert kernels of the MoE layer, gfx950.
 //
-// One launch per projection class replaces the reference's per-bucket grouped
-// launches (glm5_moe.cpp:329-405: hadamard-pre, grouped QMV, mx::sum over splits,
-// hadamard-post, clip/sigmoid/multiply, take/concatenate). The run table built on the
-// device by the router kernel drives the grid, so there is no host round trip and no
-// member cap.
+// They replace the reference's per-bucket grouped launches (glm5_moe.cpp:329-405:
+// hadamard-pre, grouped QMV, mx::sum over splits, hadamard-post, clip/sigmoid/
+// multiply, take/concatenate). The device-side run table drives the grid: no host
+// round trip, no member cap, and no cross-workgroup synchronisation inside a launch.
 //
-//  k_moe_gate_up  workgroup = (run, gate|up, 128-column block, k-split). Each pass of
-//                 up to 4 rows of the run: input Hadamard of the token rows into LDS,
-//                 the QMV wave loop, the wave sum into a split partial. The last of the
-//                 2*S workgroups of a (run, block) to finish (completion counter) sums
-//                 the splits in order, applies the output Hadamards with svh, SwiGLU
-//                 with the swiglu_limit clamp (f16 op by op), and the down projection's
-//                 input Hadamard for that 128-block, writing act_hat.
-//  k_moe_down     workgroup = (run, 128-column block, k-split) over act_hat. The last
-//                 workgroup of a (run, block) applies the output Hadamard, scales by the
-//                 routing weight (f16(f32(y) * w)); the last contribution to a
-//                 (token row, block) sums the top_k terms in rank order, adds the shared
-//                 expert and writes the layer output.
+//  k_moe_gate_up  workgroup = (run, gate|up, 128-column block), 4 waves, the whole k
+//                 range: per pass of up to 2 token rows of the run, the input
+//                 Hadamard of those rows into LDS, one k chunk per wave at a time, the
+//                 chunk partials summed in chunk order -> yhat_gu (f32, per slot).
+//                 Extra workgroups compute the f16 shared expert's down partials.
+//  k_moe_down     workgroup = (run, 128-column block), 4 waves: prologue = output
+//                 Hadamards of gate/up (svh), SwiGLU with the swiglu_limit clamp (f16 op
+//                 by op) and the down projection's input Hadamard (suh), for the whole
+//                 intermediate of each row; then the QMV over it, the output Hadamard,
+//                 and f16(f32(y) * w) per slot (or the shared expert's output).
 //
-// Per token row and expert the arithmetic is exactly exl3_trellis_linear's (same
-// input Hadamard, k partition, wave and split order, output Hadamard), so a run of r
-// rows gives the same bytes as r single-row calls.
+// Per token row and expert the arithmetic is exl3_trellis_linear's (same input
+// Hadamard, k chunks and chunk order, output Hadamard), so a run of r rows gives the
+// same bytes as r single-row calls, and a layer call the same bytes as its experts
+// evaluated one linear at a time.
 #include <hip/hip_runtime.h>
 
 #include "exl3_device.hpp"
 #include "exl3_internal.hpp"
 #include "moe_common.hpp"
+#include "moe_dense.hpp"
 #include "qmv_core.hpp"
 
 using namespace exl3d;
 using exl3m::MoeArgs;
 
 namespace {
-
-constexpr int kXsRow = kQmvMaxKtPerWg * 8;  // LDS words per staged row
 
 __device__ __forceinline__ float lo16(uint32_t v) { return (float)bitcast<f16>((uint16_t)(v & 0xffffu)); }
 __device__ __forceinline__ float hi16(uint32_t v) { return (float)bitcast<f16>((uint16_t)(v >> 16)); }
@@ -54,8 +51,15 @@ __device__ __forceinline__ float swiglu1(float g, float u, float L) {
   return rf16(act * u);
 }
 
+constexpr int kGuThreads = 256;
+constexpr int kDnThreads = 256;
+// Token rows per pass of an expert kernel. At decode batch sizes nearly every run has
+// one or two rows; a longer run takes more passes over its (L2-resident) tile range.
+constexpr int kRowsPerPass = 2;
+static_assert(kRowsPerPass <= kMaxRowsPerPass, "row pass");
+
 struct RunInfo {
-  int e, off, len, cidx;
+  int e, off, len;
 };
 
 __device__ __forceinline__ bool run_info(const MoeArgs &a, int u, int shared_mode, RunInfo &ri) {
@@ -64,227 +68,167 @@ __device__ __forceinline__ bool run_info(const MoeArgs &a, int u, int shared_mod
     ri.e = a.E;
     ri.off = a.P;
     ri.len = a.N;
-    ri.cidx = a.R;
     return true;
   }
   if (u >= *a.n_runs) return false;
   ri.e = a.run_expert[u];
   ri.off = a.run_off[u];
   ri.len = a.run_len[u];
-  ri.cidx = u;
   return true;
 }
 
-// One pass of nr <= MB rows: wave loop on the staged xs, wave sum, partial write.
+// Waves [0, nwaves) take chunks wave, wave + nwaves, ...; each chunk partial goes to
+// part[c][r][col] in LDS.
 template <int K, int CB, int MB>
-__device__ __forceinline__ void expert_pass(const uint32_t *base, int tiles_n, int cb, int k0,
-                                            int T, const uint32_t *xs, float *red, int nr,
-                                            float *dst, int64_t dst_row_stride) {
+__device__ __forceinline__ void run_chunks(const uint32_t *base, int tiles_n, int cb,
+                                           int n_chunks, int ct, int nwaves,
+                                           const uint32_t *xs, int xs_stride, float *part) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float acc[MB][2];
-  qmv_wave_loop<K, CB, MB>(base, tiles_n, cb * 8 + (lane >> 3), lane & 7, k0 + wave * T, T, wave,
-                           xs, acc);
-  qmv_stash<MB>(red, wave, lane, acc);
-  __syncthreads();
-  for (int i = threadIdx.x; i < nr * 128; i += 256) {
-    const int r = i >> 7, c = i & 127;
-    dst[r * dst_row_stride + cb * 128 + c] = qmv_wave_sum<MB>(red, r, c);
+  for (int c = wave; c < n_chunks; c += nwaves) {
+    float acc[MB][2];
+    qmv_chunk<K, CB, MB>(base, tiles_n, cb * 8 + (lane >> 3), lane & 7, c * ct, ct, xs,
+                         xs_stride, c * ct, acc);
+#pragma unroll
+    for (int r = 0; r < MB; ++r) {
+      part[(c * kRowsPerPass + r) * 128 + lane_col(lane, 0)] = acc[r][0];
+      part[(c * kRowsPerPass + r) * 128 + lane_col(lane, 1)] = acc[r][1];
+    }
   }
 }
 
 template <int K, int CB>
-__device__ __forceinline__ void expert_pass_rt(const uint32_t *base, int tiles_n, int cb, int k0,
-                                               int T, const uint32_t *xs, float *red, int nr,
-                                               float *dst, int64_t dst_row_stride) {
+__device__ __forceinline__ void run_chunks_rt(int nr, const uint32_t *base, int tiles_n, int cb,
+                                              int n_chunks, int ct, int nwaves,
+                                              const uint32_t *xs, int xs_stride, float *part) {
   if (nr == 1)
-    expert_pass<K, CB, 1>(base, tiles_n, cb, k0, T, xs, red, nr, dst, dst_row_stride);
-  else if (nr == 2)
-    expert_pass<K, CB, 2>(base, tiles_n, cb, k0, T, xs, red, nr, dst, dst_row_stride);
+    run_chunks<K, CB, 1>(base, tiles_n, cb, n_chunks, ct, nwaves, xs, xs_stride, part);
   else
-    expert_pass<K, CB, 4>(base, tiles_n, cb, k0, T, xs, red, nr, dst, dst_row_stride);
+    run_chunks<K, CB, 2>(base, tiles_n, cb, n_chunks, ct, nwaves, xs, xs_stride, part);
 }
 
+__device__ __forceinline__ float chunk_sum(const float *part, int n_chunks, int r, int col) {
+  float v = part[r * 128 + col];
+  for (int c = 1; c < n_chunks; ++c) v += part[(c * kRowsPerPass + r) * 128 + col];
+  return v;
+}
+
+
 template <int K, int CB>
-__global__ __launch_bounds__(256) void k_moe_gate_up(MoeArgs a, int shared_mode) {
-  __shared__ uint32_t xs[4 * kXsRow];
-  __shared__ float red[kQmvWaves * 4 * 128];
-  __shared__ int s_last;
+__global__ __launch_bounds__(kGuThreads) void k_moe_gate_up(MoeArgs a, int shared_mode,
+                                                            int routed_blocks) {
+  extern __shared__ uint32_t smem[];
+  if (!shared_mode && (int)blockIdx.x >= routed_blocks) {
+    // f16 shared expert down partials: H/128 column blocks x 256-row k splits of SI
+    static_assert(kGuThreads == 256, "dense_skinny runs on 4 waves");
+    const int b = blockIdx.x - routed_blocks;
+    const int n_cb = a.H / 128;
+    dense_skinny(a.dsh_act, a.N, a.SI, a.H, a.sh_dense[2], a.dsh_dn, b % n_cb, b / n_cb, smem);
+    return;
+  }
   const int out = shared_mode ? a.SI : a.I;
   const int n_cb = out / 128;
-  const int k_tiles = a.H / 16;
-  const int T = qmv_T(k_tiles), S = k_tiles / (kQmvWaves * T), kt_wg = kQmvWaves * T;
-  const int per_run = 2 * n_cb * S;
-  const int u = blockIdx.x / per_run;
-  int rem = blockIdx.x % per_run;
-  const int proj = rem / (n_cb * S);
-  rem %= n_cb * S;
-  const int cb = rem % n_cb, s = rem / n_cb;
+  const int u = blockIdx.x / (2 * n_cb);
+  const int proj = (blockIdx.x / n_cb) % 2;
+  const int cb = blockIdx.x % n_cb;
   RunInfo ri;
   if (!run_info(a, u, shared_mode, ri)) return;
   const exl3m::ExpertTab &tb = a.tab[ri.e];
   const uint32_t *base = tb.tr[proj];
   const uint16_t *suh = tb.suh[proj];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int k0 = s * kt_wg;
-  const int nblk = kt_wg / 8;  // Hadamard blocks in this workgroup's k range
-  const int64_t slot_stride = (int64_t)2 * a.Sgu * a.Imax;
+  const int k_tiles = a.H / 16, ct = chunk_tiles(k_tiles), n_chunks = k_tiles / ct;
+  const int xs_stride = a.H / 2;  // words per staged row
+  uint32_t *xs = smem;
+  float *part = reinterpret_cast<float *>(smem + kRowsPerPass * xs_stride);
+  const int nblk = a.H / 128;
 
-  for (int p0 = 0; p0 < ri.len; p0 += 4) {
-    const int nr = min(4, ri.len - p0);
-    for (int bi = wave; bi < 4 * nblk; bi += kQmvWaves) {
+  for (int p0 = 0; p0 < ri.len; p0 += kRowsPerPass) {
+    const int nr = min(kRowsPerPass, ri.len - p0);
+    for (int bi = wave; bi < kRowsPerPass * nblk; bi += kGuThreads / 64) {
       const int r = bi / nblk, blk = bi % nblk;
       uint32_t packed = 0;
       if (r < nr) {
         const int row = a.sorted_row[ri.off + p0 + r];
-        const int kc = k0 * 16 + blk * 128 + 2 * lane;
+        const int kc = blk * 128 + 2 * lane;
         const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
         const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
         float v0 = lo16(hx), v1 = hi16(hx);
         wave_had_pre(v0, v1, lo16(sx), hi16(sx));
         packed = pack16(v0, v1);
       }
-      xs[r * kXsRow + blk * 64 + lane] = packed;
+      xs[r * xs_stride + blk * 64 + lane] = packed;
     }
     __syncthreads();
-    float *dst = a.gu_part + (int64_t)(ri.off + p0) * slot_stride + (int64_t)(proj * a.Sgu + s) * a.Imax;
-    expert_pass_rt<K, CB>(base, out / 16, cb, k0, T, xs, red, nr, dst, slot_stride);
+    run_chunks_rt<K, CB>(nr, base, out / 16, cb, n_chunks, ct, kGuThreads / 64, xs, xs_stride, part);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nr * 128; i += kGuThreads) {
+      const int r = i >> 7, col = i & 127;
+      a.yhat_gu[((int64_t)(ri.off + p0 + r) * 2 + proj) * a.Imax + cb * 128 + col] =
+          chunk_sum(part, n_chunks, r, col);
+    }
     __syncthreads();
   }
-
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = atomicAdd(&a.gu_cnt[ri.cidx * a.cnt_stride + cb], 1u) == (unsigned)(2 * S - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  const int c = cb * 128 + 2 * lane;
-  const uint32_t svg = *reinterpret_cast<const uint32_t *>(tb.svh[0] + c);
-  const uint32_t svu = *reinterpret_cast<const uint32_t *>(tb.svh[1] + c);
-  const uint32_t sud = *reinterpret_cast<const uint32_t *>(tb.suh[2] + c);
-  const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
-  for (int i = wave; i < ri.len; i += kQmvWaves) {
-    const int64_t slot = ri.off + i;
-    const float *pg = a.gu_part + slot * slot_stride + c;
-    const float *pu = pg + (int64_t)a.Sgu * a.Imax;
-    float g0 = pg[0], g1 = pg[1], u0 = pu[0], u1 = pu[1];
-    for (int k = 1; k < S; ++k) {
-      g0 += pg[(int64_t)k * a.Imax];
-      g1 += pg[(int64_t)k * a.Imax + 1];
-      u0 += pu[(int64_t)k * a.Imax];
-      u1 += pu[(int64_t)k * a.Imax + 1];
-    }
-    wave_had_post(g0, g1, lo16(svg), hi16(svg));
-    wave_had_post(u0, u1, lo16(svu), hi16(svu));
-    float a0 = swiglu1(rf16(g0), rf16(u0), L);
-    float a1 = swiglu1(rf16(g1), rf16(u1), L);
-    wave_had_pre(a0, a1, lo16(sud), hi16(sud));
-    *reinterpret_cast<uint32_t *>(a.act_hat + slot * a.Imax + c) = pack16(a0, a1);
-  }
-  if (threadIdx.x == 0) a.gu_cnt[ri.cidx * a.cnt_stride + cb] = 0;
 }
 
 template <int K, int CB>
-__global__ __launch_bounds__(256) void k_moe_down(MoeArgs a, int shared_mode) {
-  __shared__ uint32_t xs[4 * kXsRow];
-  __shared__ float red[kQmvWaves * 4 * 128];
-  __shared__ int s_last;
-  __shared__ int s_rows[256];
+__global__ __launch_bounds__(kDnThreads) void k_moe_down(MoeArgs a, int shared_mode) {
+  extern __shared__ uint32_t smem[];
   const int in = shared_mode ? a.SI : a.I;
   const int n_cb = a.H / 128;
-  const int k_tiles = in / 16;
-  const int T = qmv_T(k_tiles), S = k_tiles / (kQmvWaves * T), kt_wg = kQmvWaves * T;
-  const int per_run = n_cb * S;
-  const int u = blockIdx.x / per_run;
-  const int rem = blockIdx.x % per_run;
-  const int cb = rem % n_cb, s = rem / n_cb;
+  const int u = blockIdx.x / n_cb, cb = blockIdx.x % n_cb;
   RunInfo ri;
   if (!run_info(a, u, shared_mode, ri)) return;
   const exl3m::ExpertTab &tb = a.tab[ri.e];
-  const uint32_t *base = tb.tr[2];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int k0 = s * kt_wg;
-  const int64_t slot_stride = (int64_t)a.Sdn * a.H;
+  const int k_tiles = in / 16, ct = chunk_tiles(k_tiles), n_chunks = k_tiles / ct;
+  const int xs_stride = in / 2;
+  uint32_t *xs = smem;
+  float *part = reinterpret_cast<float *>(smem + kRowsPerPass * xs_stride);
+  const int nblk = in / 128;
+  const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
 
-  for (int p0 = 0; p0 < ri.len; p0 += 4) {
-    const int nr = min(4, ri.len - p0);
-    for (int i = threadIdx.x; i < 4 * kt_wg * 8; i += 256) {
-      const int r = i / (kt_wg * 8), wd = i % (kt_wg * 8);
-      uint32_t v = 0;
-      if (r < nr)
-        v = reinterpret_cast<const uint32_t *>(a.act_hat + (int64_t)(ri.off + p0 + r) * a.Imax +
-                                               k0 * 16)[wd];
-      xs[r * kXsRow + wd] = v;
-    }
-    __syncthreads();
-    float *dst = a.dn_part + (int64_t)(ri.off + p0) * slot_stride + (int64_t)s * a.H;
-    expert_pass_rt<K, CB>(base, a.H / 16, cb, k0, T, xs, red, nr, dst, slot_stride);
-    __syncthreads();
-  }
-
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = atomicAdd(&a.dn_cnt[ri.cidx * a.cnt_stride + cb], 1u) == (unsigned)(S - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  const int c = cb * 128 + 2 * lane;
-  const uint32_t svd = *reinterpret_cast<const uint32_t *>(tb.svh[2] + c);
-  for (int i = wave; i < ri.len; i += kQmvWaves) {
-    const int64_t slot = ri.off + i;
-    const float *pd = a.dn_part + slot * slot_stride + c;
-    float y0 = pd[0], y1 = pd[1];
-    for (int k = 1; k < S; ++k) {
-      y0 += pd[(int64_t)k * a.H];
-      y1 += pd[(int64_t)k * a.H + 1];
-    }
-    wave_had_post(y0, y1, lo16(svd), hi16(svd));
-    if (shared_mode) {
-      *reinterpret_cast<uint32_t *>(a.sh_out + (int64_t)i * a.H + c) = pack16(y0, y1);
-    } else {
-      const int row = a.sorted_row[slot], rank = a.sorted_rank[slot];
-      const float w = a.weights[(int64_t)row * a.topk + rank];
-      *reinterpret_cast<uint32_t *>(a.yw + slot * a.H + c) = pack16(rf16(y0) * w, rf16(y1) * w);
-    }
-  }
-  if (threadIdx.x == 0) a.dn_cnt[ri.cidx * a.cnt_stride + cb] = 0;
-  if (shared_mode) return;
-
-  // Combine: the last of a token row's top_k contributions to this block writes it.
-  __threadfence();
-  __syncthreads();
-  for (int c0 = 0; c0 < ri.len; c0 += 256) {
-    const int nloc = min(256, ri.len - c0);
-    if ((int)threadIdx.x < nloc) {
-      const int row = a.sorted_row[ri.off + c0 + threadIdx.x];
-      const unsigned old = atomicAdd(&a.comb_cnt[(int64_t)row * n_cb + cb], 1u);
-      s_rows[threadIdx.x] = old == (unsigned)(a.topk - 1) ? row : -1;
-    }
-    __syncthreads();
-    for (int i = wave; i < nloc; i += kQmvWaves) {
-      const int row = s_rows[i];
-      if (row < 0) continue;
-      __threadfence();
-      float r0 = 0.0f, r1 = 0.0f;
-      for (int k = 0; k < a.topk; ++k) {
-        const int sl = a.slot[(int64_t)row * a.topk + k];
-        const uint32_t v = __builtin_nontemporal_load(
-            reinterpret_cast<const uint32_t *>(a.yw + (int64_t)sl * a.H + c));
-        r0 += lo16(v);
-        r1 += hi16(v);
+  for (int p0 = 0; p0 < ri.len; p0 += kRowsPerPass) {
+    const int nr = min(kRowsPerPass, ri.len - p0);
+    // SwiGLU of the gate/up outputs and the down input Hadamard, per 128-block.
+    for (int bi = wave; bi < kRowsPerPass * nblk; bi += kDnThreads / 64) {
+      const int r = bi / nblk, blk = bi % nblk;
+      uint32_t packed = 0;
+      if (r < nr) {
+        const int64_t slot = ri.off + p0 + r;
+        const int c = blk * 128 + 2 * lane;
+        const float *yg = a.yhat_gu + (slot * 2 + 0) * a.Imax + c;
+        const float *yu = a.yhat_gu + (slot * 2 + 1) * a.Imax + c;
+        float g0 = yg[0], g1 = yg[1], u0 = yu[0], u1 = yu[1];
+        const uint32_t svg = *reinterpret_cast<const uint32_t *>(tb.svh[0] + c);
+        const uint32_t svu = *reinterpret_cast<const uint32_t *>(tb.svh[1] + c);
+        const uint32_t sud = *reinterpret_cast<const uint32_t *>(tb.suh[2] + c);
+        wave_had_post(g0, g1, lo16(svg), hi16(svg));
+        wave_had_post(u0, u1, lo16(svu), hi16(svu));
+        float a0 = swiglu1(rf16(g0), rf16(u0), L);
+        float a1 = swiglu1(rf16(g1), rf16(u1), L);
+        wave_had_pre(a0, a1, lo16(sud), hi16(sud));
+        packed = pack16(a0, a1);
       }
-      r0 = rf16(r0);
-      r1 = rf16(r1);
-      if (a.has_shared) {
-        const uint32_t sv = *reinterpret_cast<const uint32_t *>(a.sh_out + (int64_t)row * a.H + c);
-        r0 += lo16(sv);
-        r1 += hi16(sv);
+      xs[r * xs_stride + blk * 64 + lane] = packed;
+    }
+    __syncthreads();
+    run_chunks_rt<K, CB>(nr, tb.tr[2], a.H / 16, cb, n_chunks, ct, kDnThreads / 64, xs, xs_stride,
+                         part);
+    __syncthreads();
+    const int c = cb * 128 + 2 * lane;
+    const uint32_t svd = *reinterpret_cast<const uint32_t *>(tb.svh[2] + c);
+    for (int r = wave; r < nr; r += kDnThreads / 64) {
+      float y0 = chunk_sum(part, n_chunks, r, 2 * lane);
+      float y1 = chunk_sum(part, n_chunks, r, 2 * lane + 1);
+      wave_had_post(y0, y1, lo16(svd), hi16(svd));
+      const int64_t slot = ri.off + p0 + r;
+      if (shared_mode) {
+        *reinterpret_cast<uint32_t *>(a.sh_out + (slot - a.P) * a.H + c) = pack16(y0, y1);
+      } else {
+        const int row = a.sorted_row[slot], rank = a.sorted_rank[slot];
+        const float w = a.weights[(int64_t)row * a.topk + rank];
+        *reinterpret_cast<uint32_t *>(a.yw + slot * a.H + c) = pack16(rf16(y0) * w, rf16(y1) * w);
       }
-      *reinterpret_cast<uint32_t *>(a.out + (int64_t)row * a.H + c) = pack16(r0, r1);
-      if (lane == 0) a.comb_cnt[(int64_t)row * n_cb + cb] = 0;
     }
     __syncthreads();
   }
@@ -294,30 +238,61 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a, int shared_mode) {
 
 namespace exl3h {
 
-template <int K, int CB>
-static void moe_go(int which, dim3 grid, hipStream_t st, const MoeArgs &a, int shared_mode) {
-  if (which == 0)
-    k_moe_gate_up<K, CB><<<grid, 256, 0, st>>>(a, shared_mode);
-  else
-    k_moe_down<K, CB><<<grid, 256, 0, st>>>(a, shared_mode);
+size_t moe_gate_up_lds(int H) {
+  const int k_tiles = H / 16;
+  return (size_t)kRowsPerPass * (H / 2) * 4 + (size_t)(k_tiles / chunk_tiles(k_tiles)) *
+                                                      kRowsPerPass * 128 * 4;
 }
 
-// which: 0 = gate/up, 1 = down.
+size_t moe_down_lds(int in) {
+  const int k_tiles = in / 16;
+  return (size_t)kRowsPerPass * (in / 2) * 4 + (size_t)(k_tiles / chunk_tiles(k_tiles)) *
+                                                       kRowsPerPass * 128 * 4;
+}
+
+template <int K, int CB>
+static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
+                          int shared_mode, int routed_blocks) {
+  if (which == 0) {
+    const size_t lds = std::max(moe_gate_up_lds(a.H), (size_t)4 * kDenseLdsWords);
+    static bool attr_set = false;
+    if (!attr_set) {
+      EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_gate_up<K, CB>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      attr_set = true;
+    }
+    k_moe_gate_up<K, CB><<<blocks, kGuThreads, lds, st>>>(a, shared_mode, routed_blocks);
+  } else {
+    const size_t lds = moe_down_lds(shared_mode ? a.SI : a.I);
+    static bool attr_set = false;
+    if (!attr_set) {
+      EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_down<K, CB>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      attr_set = true;
+    }
+    k_moe_down<K, CB><<<blocks, kDnThreads, lds, st>>>(a, shared_mode);
+  }
+  return EXL3_OK;
+}
+
+// which: 0 = gate/up (routed_blocks = workgroups of routed runs; the rest compute the
+// f16 shared expert's down partials), 1 = down.
 exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const MoeArgs &a,
-                              int shared_mode, hipStream_t st) {
+                              int shared_mode, int routed_blocks, hipStream_t st) {
   if (blocks == 0) return EXL3_OK;
-  dim3 grid(blocks);
-#define EXL3_KC(KK)                                                      \
-  case KK:                                                               \
-    if (cb == 0) moe_go<KK, 0>(which, grid, st, a, shared_mode);         \
-    else if (cb == 1) moe_go<KK, 1>(which, grid, st, a, shared_mode);    \
-    else moe_go<KK, 2>(which, grid, st, a, shared_mode);                 \
+  exl3_status rc = EXL3_OK;
+#define EXL3_KC(KK)                                                                          \
+  case KK:                                                                                   \
+    if (cb == 0) rc = moe_go<KK, 0>(which, blocks, st, a, shared_mode, routed_blocks);       \
+    else if (cb == 1) rc = moe_go<KK, 1>(which, blocks, st, a, shared_mode, routed_blocks);  \
+    else rc = moe_go<KK, 2>(which, blocks, st, a, shared_mode, routed_blocks);               \
     break;
   switch (K) {
     EXL3_KC(1) EXL3_KC(2) EXL3_KC(3) EXL3_KC(4) EXL3_KC(5) EXL3_KC(6) EXL3_KC(7) EXL3_KC(8)
     default: return fail(EXL3_ERR_INVALID, "K out of range");
   }
 #undef EXL3_KC
+  if (rc) return rc;
   EXL3_LAUNCHED(which == 0 ? "k_moe_gate_up" : "k_moe_down");
   return EXL3_OK;
 }

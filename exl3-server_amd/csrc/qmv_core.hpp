@@ -1,69 +1,78 @@
-// The dequant-GEMV core shared by the standalone linear and the MoE expert kernels,
-// so that every entry point that sees one tensor shape sums it in the same f32 order.
+// The dequant-GEMV core shared by the standalone linear and the MoE expert kernels.
 //
-// Workgroup = 4 waves. A workgroup owns one 128-column block (8 n-tiles) of one
-// member and a contiguous range of 4*T k-tiles; wave w streams the T k-tiles starting
-// at k0 + w*T in order, double-buffering one k-tile of ring words in registers.
-// Per output element the result is ((wave0 + wave1) + wave2) + wave3.
+// k partition (a function of the tensor's k-tile count only): the k range is cut into
+// chunks of chunk_tiles(k_tiles) consecutive k-tiles. One wave computes one chunk's
+// partial sums from zero, visiting its k-tiles in order; an output is the in-order
+// sum of its chunk partials (c = 0, 1, 2, ...). Every entry point -- standalone,
+// grouped, MoE -- follows this order, so they agree bit for bit on a shape, whatever
+// workgroup or launch a chunk ran in.
+//
+// A wave covers 8 n-tiles (128 output columns, one Hadamard block) of one member; lane
+// l holds columns (l/8)*16 + l%8 and that + 8 (see exl3_device.hpp).
 #pragma once
 
 #include "exl3_device.hpp"
 
 namespace exl3d {
 
-constexpr int kQmvWaves = 4;
-constexpr int kQmvMaxKtPerWg = 64;  // 4 waves x at most 16 k-tiles
+constexpr int kMaxRowsPerPass = 4;
 
-// xs: LDS, MB rows of (4*T k-tiles x 16) f16 packed as u32 pairs; row stride
-// kQmvMaxKtPerWg * 8 words. Rows past the valid count must hold zeros.
-template <int K, int CB, int MB>
-__device__ __forceinline__ void qmv_wave_loop(const uint32_t *__restrict__ base, int tiles_n,
-                                              int tn, int m, int kw, int T, int wave,
-                                              const uint32_t *xs, float (&acc)[MB][2]) {
+__host__ __device__ constexpr int chunk_tiles(int k_tiles) { return (k_tiles % 16 == 0) ? 16 : 8; }
+
+typedef const __attribute__((address_space(1))) uint32_t *gu32p;
+
+template <int K>
+__device__ __forceinline__ void lane_load_g(gu32p tile, int m, uint32_t (&W)[K + 1]) {
+  gu32p p = tile + m * K;
 #pragma unroll
-  for (int r = 0; r < MB; ++r) acc[r][0] = acc[r][1] = 0.0f;
-  uint32_t Wc[K + 1], Wn[K + 1];
-  lane_load<K>(base + ((int64_t)kw * tiles_n + tn) * 8 * K, m, Wc);
-  for (int t = 0; t < T; ++t) {
-    if (t + 1 < T) lane_load<K>(base + ((int64_t)(kw + t + 1) * tiles_n + tn) * 8 * K, m, Wn);
-    uint32_t X[MB][8];
-#pragma unroll
-    for (int r = 0; r < MB; ++r)
-#pragma unroll
-      for (int u = 0; u < 8; ++u) X[r][u] = xs[r * (kQmvMaxKtPerWg * 8) + (wave * T + t) * 8 + u];
-    lane_tile_fma<K, CB, MB>(Wc, X, acc);
-#pragma unroll
-    for (int w = 0; w <= K; ++w) Wc[w] = Wn[w];
-  }
+  for (int w = 0; w < K; ++w) W[w + 1] = __builtin_nontemporal_load(p + w);
+  W[0] = __builtin_nontemporal_load(tile + ((m * K + 8 * K - 1) % (8 * K)));
 }
 
-// Lane l of a wave holds columns (l/8)*16 + l%8 (acc[r][0]) and that + 8 (acc[r][1]).
+// x values of k-tile kt for MB rows from LDS: xs row r holds 8 packed f16 pairs per
+// k-tile starting at word kt * 8 (row stride `stride` words).
 template <int MB>
-__device__ __forceinline__ void qmv_stash(float *red /* [4][MB][128] */, int wave, int lane,
-                                          const float (&acc)[MB][2]) {
-  const int c = (lane >> 3) * 16 + (lane & 7);
+__device__ __forceinline__ void load_x(const uint32_t *xs, int stride, int kt,
+                                       uint32_t (&X)[MB][8]) {
 #pragma unroll
   for (int r = 0; r < MB; ++r) {
-    red[(wave * MB + r) * 128 + c] = acc[r][0];
-    red[(wave * MB + r) * 128 + c + 8] = acc[r][1];
+    const uint4 a = *reinterpret_cast<const uint4 *>(xs + r * stride + kt * 8);
+    const uint4 b = *reinterpret_cast<const uint4 *>(xs + r * stride + kt * 8 + 4);
+    X[r][0] = a.x; X[r][1] = a.y; X[r][2] = a.z; X[r][3] = a.w;
+    X[r][4] = b.x; X[r][5] = b.y; X[r][6] = b.z; X[r][7] = b.w;
   }
 }
 
-template <int MB>
-__device__ __forceinline__ float qmv_wave_sum(const float *red, int r, int c) {
-  float v = red[(0 * MB + r) * 128 + c];
-  v += red[(1 * MB + r) * 128 + c];
-  v += red[(2 * MB + r) * 128 + c];
-  v += red[(3 * MB + r) * 128 + c];
-  return v;
+// One chunk: acc = sum over k-tiles [kt0, kt0 + nkt) of this lane's 32 weights times x,
+// from zero. `base` = member's trellis words, tn = this lane's n-tile, m = lane slot in
+// its tile; xs/xkt0: the LDS x row holding k-tile kt0 at word offset xkt0 * 8.
+// Two k-tiles of ring words are kept in flight per lane (nkt is even).
+template <int K, int CB, int MB>
+__device__ __forceinline__ void qmv_chunk(const uint32_t *base, int tiles_n, int tn, int m,
+                                          int kt0, int nkt, const uint32_t *xs, int stride,
+                                          int xkt0, float (&acc)[MB][2]) {
+#pragma unroll
+  for (int r = 0; r < MB; ++r) acc[r][0] = acc[r][1] = 0.0f;
+  gu32p g = (gu32p)base;
+  const int64_t tstride = (int64_t)tiles_n * 8 * K;  // words between consecutive k-tiles
+  gu32p t0 = g + ((int64_t)kt0 * tiles_n + tn) * 8 * K;
+  uint32_t Wa[K + 1], Wb[K + 1];
+  lane_load_g<K>(t0, m, Wa);
+  lane_load_g<K>(t0 + tstride, m, Wb);
+  for (int t = 0; t < nkt; t += 2) {
+    uint32_t X[MB][8];
+    load_x<MB>(xs, stride, xkt0 + t, X);
+    lane_tile_fma<K, CB, MB>(Wa, X, acc);
+    if (t + 2 < nkt) lane_load_g<K>(t0 + (t + 2) * tstride, m, Wa);
+    load_x<MB>(xs, stride, xkt0 + t + 1, X);
+    lane_tile_fma<K, CB, MB>(Wb, X, acc);
+    if (t + 3 < nkt) lane_load_g<K>(t0 + (t + 3) * tstride, m, Wb);
+  }
 }
 
-// The k partition (mirrors exl3h::kpart on the host).
-__device__ __forceinline__ int qmv_T(int k_tiles) {
-  if (k_tiles >= 256 && k_tiles % 64 == 0) return 16;
-  if (k_tiles % 32 == 0) return 8;
-  if (k_tiles % 16 == 0) return 4;
-  return 2;
+// Column of acc[r][h] inside the wave's 128-column block.
+__device__ __forceinline__ int lane_col(int lane, int h) {
+  return (lane >> 3) * 16 + (lane & 7) + 8 * h;
 }
 
 }  // namespace exl3d

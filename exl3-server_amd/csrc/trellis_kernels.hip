@@ -134,52 +134,52 @@ __global__ __launch_bounds__(256) void k_hadamard(const uint16_t *__restrict__ x
 }
 
 // ---------------------------------------------------------------------------------
-// QMV: grid (n_cb * S, row passes, members); 4 waves per workgroup. Workgroup (cb, s)
-// owns output columns [cb*128, cb*128+128) and k-tiles [s*4T, s*4T + 4T); wave w takes
-// the T consecutive k-tiles starting at s*4T + w*T. Output: f32 partials
-// part[member][s][row][col], each the in-order sum of the four waves' partials.
+// QMV: grid (n_cb * ceil(n_chunks / 4), row passes, members); 4 waves per workgroup,
+// one k chunk per wave. Workgroup (cb, g) owns output columns [cb*128, cb*128+128) and
+// chunks [4g, 4g+4); each wave writes its chunk partial part[member][chunk][row][col].
 // ---------------------------------------------------------------------------------
 template <int K, int CB, int MB>
 __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_n, int in,
-                                             int out, int T, int S,
-                                             const uint16_t *__restrict__ xhat,
+                                             int out, const uint16_t *__restrict__ xhat,
                                              int64_t x_member_stride, int64_t rows,
                                              float *__restrict__ part) {
-  __shared__ uint32_t xs[MB * kQmvMaxKtPerWg * 8];
-  __shared__ float red[kQmvWaves * MB * 128];
+  constexpr int kXsRow = 4 * 16 * 8;  // 4 chunks of at most 16 k-tiles, 8 words each
+  __shared__ uint32_t xs[MB * kXsRow];
+  const int k_tiles = in / 16, ct = chunk_tiles(k_tiles), n_chunks = k_tiles / ct;
   const int n_cb = out / 128;
-  const int cb = blockIdx.x % n_cb, s = blockIdx.x / n_cb;
+  const int cb = blockIdx.x % n_cb, g = blockIdx.x / n_cb;
   const int64_t r0 = (int64_t)blockIdx.y * MB;
   const int member = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int kt_wg = kQmvWaves * T;
-  const int k0 = s * kt_wg;
+  const int c0 = g * 4;
+  const int nc = min(4, n_chunks - c0);
+  const int kt_wg = nc * ct;
 
   const uint16_t *xm = xhat + member * x_member_stride;
   for (int i = threadIdx.x; i < MB * kt_wg * 8; i += 256) {
     const int r = i / (kt_wg * 8), wd = i % (kt_wg * 8);
     uint32_t v = 0;
-    if (r0 + r < rows) v = reinterpret_cast<const uint32_t *>(xm + (r0 + r) * in + k0 * 16)[wd];
-    xs[r * kQmvMaxKtPerWg * 8 + wd] = v;
+    if (r0 + r < rows) v = reinterpret_cast<const uint32_t *>(xm + (r0 + r) * in + c0 * ct * 16)[wd];
+    xs[r * kXsRow + wd] = v;
   }
   __syncthreads();
-
+  if (wave >= nc) return;
   float acc[MB][2];
-  qmv_wave_loop<K, CB, MB>((const uint32_t *)trellis.p[member], tiles_n, cb * 8 + (lane >> 3),
-                           lane & 7, k0 + wave * T, T, wave, xs, acc);
-  qmv_stash<MB>(red, wave, lane, acc);
-  __syncthreads();
-  for (int i = threadIdx.x; i < MB * 128; i += 256) {
-    const int r = i >> 7, c = i & 127;
-    if (r0 + r >= rows) continue;
-    part[(((int64_t)member * S + s) * rows + r0 + r) * out + cb * 128 + c] =
-        qmv_wave_sum<MB>(red, r, c);
+  qmv_chunk<K, CB, MB>((const uint32_t *)trellis.p[member], tiles_n, cb * 8 + (lane >> 3),
+                       lane & 7, (c0 + wave) * ct, ct, xs, kXsRow, wave * ct, acc);
+  const int chunk = c0 + wave;
+#pragma unroll
+  for (int r = 0; r < MB; ++r) {
+    if (r0 + r >= rows) break;
+    float *p = part + (((int64_t)member * n_chunks + chunk) * rows + r0 + r) * out + cb * 128;
+    p[lane_col(lane, 0)] = acc[r][0];
+    p[lane_col(lane, 1)] = acc[r][1];
   }
 }
 
-// One wave per (member, row, 128-column block): split sum in split order, then the raw
-// f32 result or the output Hadamard.
-__global__ __launch_bounds__(256) void k_qmv_finalize(int n, int S, int64_t rows, int out,
+// One wave per (member, row, 128-column block): chunk partials summed in chunk order,
+// then the raw f32 result or the output Hadamard.
+__global__ __launch_bounds__(256) void k_qmv_finalize(int n, int n_chunks, int64_t rows, int out,
                                                       const float *__restrict__ part,
                                                       float *__restrict__ y32,
                                                       uint16_t *__restrict__ y16,
@@ -193,16 +193,11 @@ __global__ __launch_bounds__(256) void k_qmv_finalize(int n, int S, int64_t rows
   const int64_t row = rest % rows;
   const int member = (int)(rest / rows);
   const int c = cb * 128 + 2 * lane;
-  float v0 = 0.0f, v1 = 0.0f;
-  for (int s = 0; s < S; ++s) {
-    const float *p = part + (((int64_t)member * S + s) * rows + row) * out + c;
-    if (s == 0) {
-      v0 = p[0];
-      v1 = p[1];
-    } else {
-      v0 += p[0];
-      v1 += p[1];
-    }
+  const float *p = part + ((int64_t)member * n_chunks * rows + row) * out + c;
+  float v0 = p[0], v1 = p[1];
+  for (int s = 1; s < n_chunks; ++s) {
+    v0 += p[(int64_t)s * rows * out];
+    v1 += p[(int64_t)s * rows * out + 1];
   }
   const int64_t o = ((int64_t)member * rows + row) * out + c;
   if (y32) {
@@ -264,29 +259,27 @@ exl3_status launch_hadamard(const uint16_t *x16, const float *x32, int64_t rows,
 
 template <int K, int CB, int MB>
 static void qmv_go(dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in, int out,
-                   int T, int S, const uint16_t *xhat, int64_t xs, int64_t rows, float *part) {
-  k_qmv<K, CB, MB><<<grid, 256, 0, st>>>(tr, tiles_n, in, out, T, S, xhat, xs, rows, part);
+                   const uint16_t *xhat, int64_t xs, int64_t rows, float *part) {
+  k_qmv<K, CB, MB><<<grid, 256, 0, st>>>(tr, tiles_n, in, out, xhat, xs, rows, part);
 }
 
 template <int K, int CB>
 static void qmv_mb(int mb, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in,
-                   int out, int T, int S, const uint16_t *xhat, int64_t xs, int64_t rows,
-                   float *part) {
+                   int out, const uint16_t *xhat, int64_t xs, int64_t rows, float *part) {
   switch (mb) {
-    case 1: qmv_go<K, CB, 1>(grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
-    case 2: qmv_go<K, CB, 2>(grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
-    default: qmv_go<K, CB, 4>(grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
+    case 1: qmv_go<K, CB, 1>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
+    case 2: qmv_go<K, CB, 2>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
+    default: qmv_go<K, CB, 4>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
   }
 }
 
 template <int K>
 static void qmv_cb(int cb, int mb, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n,
-                   int in, int out, int T, int S, const uint16_t *xhat, int64_t xs, int64_t rows,
-                   float *part) {
+                   int in, int out, const uint16_t *xhat, int64_t xs, int64_t rows, float *part) {
   switch (cb) {
-    case 0: qmv_mb<K, 0>(mb, grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
-    case 1: qmv_mb<K, 1>(mb, grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
-    default: qmv_mb<K, 2>(mb, grid, st, tr, tiles_n, in, out, T, S, xhat, xs, rows, part); break;
+    case 0: qmv_mb<K, 0>(mb, grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
+    case 1: qmv_mb<K, 1>(mb, grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
+    default: qmv_mb<K, 2>(mb, grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
   }
 }
 
@@ -298,12 +291,13 @@ exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, 
   const exl3_tuning tn = tuning();
   int mb = tn.rows_per_pass > 0 ? tn.rows_per_pass : (rows >= 4 ? 4 : (int)rows);
   mb = mb >= 4 ? 4 : (mb >= 2 ? 2 : 1);
-  dim3 grid((unsigned)((out / 128) * kp.S), (unsigned)((rows + mb - 1) / mb), (unsigned)n);
+  dim3 grid((unsigned)((out / 128) * ((kp.n_chunks + 3) / 4)), (unsigned)((rows + mb - 1) / mb),
+            (unsigned)n);
   const int tiles_n = out / 16;
   switch (shape.K) {
 #define EXL3_K(KK)                                                                        \
   case KK:                                                                                \
-    qmv_cb<KK>(shape.codebook, mb, grid, st, trellis, tiles_n, in, out, kp.T, kp.S, xhat,  \
+    qmv_cb<KK>(shape.codebook, mb, grid, st, trellis, tiles_n, in, out, xhat,             \
                x_member_stride, rows, part);                                              \
     break;
     EXL3_K(1) EXL3_K(2) EXL3_K(3) EXL3_K(4) EXL3_K(5) EXL3_K(6) EXL3_K(7) EXL3_K(8)
@@ -314,11 +308,12 @@ exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, 
   return EXL3_OK;
 }
 
-exl3_status launch_qmv_finalize(int n, int S, int64_t rows, int out, const float *part,
+exl3_status launch_qmv_finalize(int n, int n_chunks, int64_t rows, int out, const float *part,
                                 float *y32, uint16_t *y16, const PtrTable &svh, hipStream_t st) {
   const int64_t waves = (int64_t)n * rows * (out / 128);
   if (waves == 0) return EXL3_OK;
-  k_qmv_finalize<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(n, S, rows, out, part, y32, y16, svh);
+  k_qmv_finalize<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(n, n_chunks, rows, out, part, y32,
+                                                              y16, svh);
   EXL3_LAUNCHED("k_qmv_finalize");
   return EXL3_OK;
 }

@@ -66,8 +66,8 @@ class MoeDiag(C.Structure):
 
 
 class MoeTiming(C.Structure):
-    _fields_ = [("calls", C.c_int64), ("router_ms", C.c_double), ("shared_ms", C.c_double),
-                ("gate_up_ms", C.c_double), ("down_ms", C.c_double), ("total_ms", C.c_double),
+    _fields_ = [("calls", C.c_int64), ("router_ms", C.c_double), ("gate_up_ms", C.c_double),
+                ("down_ms", C.c_double), ("combine_ms", C.c_double), ("total_ms", C.c_double),
                 ("gate_up_trellis_bytes", C.c_int64), ("down_trellis_bytes", C.c_int64)]
 
 

@@ -131,10 +131,10 @@ typedef struct {
  * the distinct experts each call streamed (each expert counted once per call). */
 typedef struct {
   int64_t calls;
-  double router_ms;     /* logits + top-k routing + expert-order dispatch */
-  double shared_ms;     /* shared expert */
-  double gate_up_ms;    /* routed gate|up + SwiGLU kernel */
-  double down_ms;       /* routed down + weighted combine kernel */
+  double router_ms;     /* logits + top-k routing + expert-order dispatch (+ f16 shared gate/up) */
+  double gate_up_ms;    /* routed gate|up kernel (+ f16 shared down) */
+  double down_ms;       /* routed SwiGLU + down kernel */
+  double combine_ms;    /* weighted combine (+ a trellis shared expert) */
   double total_ms;
   int64_t gate_up_trellis_bytes;
   int64_t down_trellis_bytes;

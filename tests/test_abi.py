@@ -58,11 +58,11 @@ def test_path_info_and_workspace_query():
     d = fake_desc()
     _lib.call("exl3_trellis_path_info", C.byref(d), 8, C.byref(info))
     assert info.staged == 0 and info.rows_per_block == 4 and info.passes == 2
-    assert info.splits == 4  # 256 k-tiles: 4 waves x 16 k-tiles x 4 splits
+    assert info.splits == 16  # 256 k-tiles: 16 chunks of 16 k-tiles
     ws1 = L.exl3_trellis_workspace_size(C.byref(d), 1, 1)
     ws8 = L.exl3_trellis_workspace_size(C.byref(d), 8, 3)
     assert 0 < ws1 < ws8
-    assert ws1 >= 4096 * 2 + 4 * 1024 * 4  # xhat + 4 split planes
+    assert ws1 >= 4096 * 2 + 16 * 1024 * 4  # xhat + 16 chunk planes
 
 
 def test_workspace_too_small_is_reported_before_launch():
