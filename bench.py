@@ -31,6 +31,19 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "exl3-server_amd"))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_glm5_b8_traffic.md")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from the
+    committed rocprofv3 counter summary of this same workload, or None."""
+    import re
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(rf"^{kernel} HBM bytes per dispatch \(read \+ write\): (\d+)$", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def build_layers(n_layers, seed, device):
@@ -111,6 +124,9 @@ def main():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed steps, run one plain device copy of 256 MiB (the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run here "
@@ -151,6 +167,13 @@ def main():
     gpu_ms = ev0.elapsed_time(ev1)
     ms_per_step = wall * 1e3 / args.steps
     value = B / (ms_per_step / 1e3)
+
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # Per-stage kernel time (HIP events inside the library, on the same stream) over one
     # more rotation of every layer instance, several times.
@@ -195,10 +218,12 @@ def main():
                    "layer_instances": args.layers, "parallelism": "none (one GPU)"},
         "roofline": {"kernel": "k_moe_gate_up", "bound": "hbm", "achieved": round(gu_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": round(gu_bytes),
+                     "traffic": measured_traffic("k_moe_gate_up"),
+                     "algorithmic_bytes_per_launch": round(gu_bytes),
                      "avg_launch_ms": round(gu_ms, 5)},
         "roofline_down": {"kernel": "k_moe_down", "achieved": round(dn_gbps, 1),
                           "frac": round(dn_gbps / HBM_PEAK_GBPS, 4),
+                          "traffic": measured_traffic("k_moe_down"),
                           "algorithmic_bytes_per_launch": round(dn_bytes), "avg_launch_ms": round(dn_ms, 5)},
         "routed_trellis_GBps": round(routed_gbps, 1),
         "distinct_experts_per_step": round(distinct, 2),

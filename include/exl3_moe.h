@@ -12,9 +12,9 @@
  * last failure on the calling thread. Nothing is thrown across the ABI. Shape and
  * geometry errors are detected on the host before any kernel is launched.
  *
- * Threading: calls are thread-safe for distinct streams and distinct handles. A layer
- * handle and its workspace must not be used by two in-flight calls at once (the
- * workspace holds that call's intermediate state and completion counters).
+ * Threading: calls are thread-safe for distinct streams and distinct handles. A
+ * workspace must not be used by two in-flight calls at once (it holds that call's
+ * routing, dispatch table and intermediate activations).
  */
 #ifndef EXL3_MOE_H
 #define EXL3_MOE_H
