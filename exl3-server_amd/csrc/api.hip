@@ -55,17 +55,16 @@ using namespace exl3h;
 namespace {
 
 // Workspace carve-up for the single/grouped linear: xhat f16 (n, rows, in) then the
-// chunk partials f32 (n, n_chunks, rows, out).
+// slice partials f32 (n, n_slices, rows, out).
 struct LinearWs {
   size_t xhat_off, part_off, total;
 };
 
 LinearWs linear_ws(int in, int out, int64_t rows, int n) {
-  const KPart kp = kpart(in / 16);
   LinearWs w;
   w.xhat_off = 0;
   w.part_off = align_up((size_t)n * rows * in * 2, 256);
-  w.total = w.part_off + align_up((size_t)n * kp.n_chunks * rows * out * 4, 256);
+  w.total = w.part_off + align_up((size_t)n * qmv_slices(in) * rows * out * 4, 256);
   return w;
 }
 
@@ -90,7 +89,7 @@ exl3_status linear_core(const exl3_trellis_desc *members, int n, const uint16_t 
   if (rc) return rc;
   uint16_t *xhat = reinterpret_cast<uint16_t *>((char *)ws + lw.xhat_off);
   float *part = reinterpret_cast<float *>((char *)ws + lw.part_off);
-  const KPart kp = kpart(in / 16);
+  const int n_sl = qmv_slices(in);
   for (int c0 = 0; c0 < n; c0 += PtrTable::kMax) {
     const int cn = std::min(PtrTable::kMax, n - c0);
     PtrTable tr{}, su{}, sv{};
@@ -122,7 +121,7 @@ exl3_status linear_core(const exl3_trellis_desc *members, int n, const uint16_t 
     }
     rc = launch_qmv(w0, tr, cn, xh, x_stride, rows, part, st);
     if (rc) return rc;
-    rc = launch_qmv_finalize(cn, kp.n_chunks, rows, out, part,
+    rc = launch_qmv_finalize(cn, n_sl, rows, out, part,
                              y32 ? y32 + (int64_t)c0 * rows * out : nullptr,
                              y16 ? y16 + (int64_t)c0 * rows * out : nullptr, sv, st);
     if (rc) return rc;
@@ -157,15 +156,18 @@ exl3_status exl3_trellis_path_info(const exl3_trellis_desc *w, int64_t rows,
   if (rc) return rc;
   if (!info || rows < 0) return fail(EXL3_ERR_INVALID, "bad path_info arguments");
   const exl3_tuning tn = tuning();
-  const KPart kp = kpart(w->in_features / 16);
-  int mb = tn.rows_per_pass > 0 ? tn.rows_per_pass : (rows >= 4 ? 4 : (int)rows);
-  mb = mb >= 4 ? 4 : (mb >= 2 ? 2 : 1);
-  info->staged = 0;
+  const int mb = qmv_pass_rows(rows);
+  // Every pass runs on the matrix cores; "staged" reports the reference's criterion
+  // (a pass shared by at least mat_min_rows rows, trellis_gemm.cpp:800-812).
+  info->staged = (tn.mat_min_rows > 0 && rows >= tn.mat_min_rows &&
+                  (tn.mat_max_rows <= 0 || rows <= tn.mat_max_rows))
+                     ? 1
+                     : 0;
   info->rows_per_block = mb;
   info->pad_rows = (int32_t)((rows + mb - 1) / mb * mb);
   info->passes = (int32_t)((rows + mb - 1) / mb);
-  info->splits = kp.n_chunks;
-  info->tiles_per_workgroup = 8;
+  info->splits = qmv_slices(w->in_features);
+  info->tiles_per_workgroup = 32;
   return EXL3_OK;
 }
 

@@ -32,17 +32,11 @@ inline hipStream_t stream_of(exl3_stream_t s) { return reinterpret_cast<hipStrea
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // The k partition of a trellis GEMV, a function of the tensor's k-tile count only: the
-// k range is cut into chunks of `ct` k-tiles, each summed from zero by one wave, and
-// an output is the in-order sum of its chunk partials (device side: qmv_core.hpp).
-struct KPart {
-  int ct;        // k-tiles per chunk
-  int n_chunks;  // chunks per output column
-};
-
-inline KPart kpart(int k_tiles) {
-  const int ct = (k_tiles % 16 == 0) ? 16 : 8;
-  return KPart{ct, k_tiles / ct};
-}
+// k range is cut into slices, each summed from zero by one wave, and an output is the
+// in-order sum of its slice partials (device side: qmv_core.hpp).
+int qmv_slices(int in);
+// Token rows per MFMA pass of the standalone/grouped linear (rows_per_pass knob, <= 16).
+int qmv_pass_rows(int64_t rows);
 
 // Scheduling knobs (exl3_set_tuning).
 exl3_tuning tuning();
@@ -66,13 +60,13 @@ exl3_status launch_hadamard(const uint16_t *x16, const float *x32, int64_t rows,
                             hipStream_t st);
 
 // xhat: (n, rows, in) f16 (member stride rows*in, or 0 when shared); part: f32
-// (n, n_chunks, rows, out).
+// (n, n_slices, rows, out).
 exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, int n,
                        const uint16_t *xhat, int64_t x_member_stride, int64_t rows, float *part,
                        hipStream_t st);
-// Sums the chunk partials in chunk order into y32 (raw f32, (n, rows, out)) or, through
+// Sums the slice partials in slice order into y32 (raw f32, (n, rows, out)) or, through
 // the output Hadamard with member m's svh.p[m], into y16 (n, rows, out).
-exl3_status launch_qmv_finalize(int n, int n_chunks, int64_t rows, int out, const float *part,
+exl3_status launch_qmv_finalize(int n, int n_sl, int64_t rows, int out, const float *part,
                                 float *y32, uint16_t *y16, const PtrTable &svh,
                                 hipStream_t st);
 

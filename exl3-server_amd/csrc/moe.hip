@@ -15,6 +15,7 @@
 #include "exl3_moe.h"
 #include "moe_common.hpp"
 #include "moe_dense.hpp"
+#include "qmv_core.hpp"
 
 using namespace exl3d;
 using exl3m::ExpertTab;
@@ -23,6 +24,8 @@ using exl3m::MoeArgs;
 namespace exl3h {
 exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const MoeArgs &a,
                               int shared_mode, int routed_blocks, hipStream_t st);
+int moe_slices(int in);
+exl3_status launch_moe_act(const MoeArgs &a, int shared_mode, int dense_blocks, hipStream_t st);
 }
 
 namespace {
@@ -310,10 +313,27 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
 }
 
 // ---------------------------------------------------------------------------------
-// L5. Combine (glm5_moe.cpp:411-416): one wave per (token row, 128-column block):
-// routed = f16(sum over ranks, in rank order, of the slots' f16(y * w)), then
+// L6. Combine (glm5_moe.cpp:369-416): one wave per (token row, 128-column block). Per
+// rank k (in rank order): the slot's down slice partials summed in slice order, the
+// output Hadamard with the expert's svh, y = f16 (the linear's output), then
+// f16(f32(y) * w_k); routed = f16(sum of those f16 terms in rank order), then
 // out = f16(routed + shared).
 // ---------------------------------------------------------------------------------
+__device__ __forceinline__ void down_out(const MoeArgs &a, int64_t slot, int n_sl,
+                                         const uint16_t *svh, int c, float &y0, float &y1) {
+  const float *p = a.yhat_dn + slot * a.S_dn * a.H + c;
+  y0 = p[0];
+  y1 = p[1];
+  for (int s = 1; s < n_sl; ++s) {
+    y0 += p[(int64_t)s * a.H];
+    y1 += p[(int64_t)s * a.H + 1];
+  }
+  const uint32_t sv = *reinterpret_cast<const uint32_t *>(svh + c);
+  wave_had_post(y0, y1, lo16(sv), hi16(sv));
+  y0 = rf16(y0);
+  y1 = rf16(y1);
+}
+
 __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   const int lane = threadIdx.x & 63;
   const int n_cb = a.H / 128;
@@ -321,19 +341,24 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   if (gw >= (int64_t)a.N * n_cb) return;
   const int row = (int)(gw / n_cb), cb = (int)(gw % n_cb);
   const int c = cb * 128 + 2 * lane;
+  const int n_sl = n_slices(a.I / 16);
   float r0 = 0.0f, r1 = 0.0f;
   for (int k = 0; k < a.topk; ++k) {
-    const int sl = a.slot[(int64_t)row * a.topk + k];
-    const uint32_t v = *reinterpret_cast<const uint32_t *>(a.yw + (int64_t)sl * a.H + c);
-    r0 += lo16(v);
-    r1 += hi16(v);
+    const int64_t pk = (int64_t)row * a.topk + k;
+    const int e = a.ids[pk];
+    const float w = a.weights[pk];
+    float y0, y1;
+    down_out(a, a.slot[pk], n_sl, a.tab[e].svh[2], c, y0, y1);
+    r0 += rf16(y0 * w);
+    r1 += rf16(y1 * w);
   }
   r0 = rf16(r0);
   r1 = rf16(r1);
   if (a.shared_kind == exl3m::kSharedTrellis) {
-    const uint32_t sv = *reinterpret_cast<const uint32_t *>(a.sh_out + (int64_t)row * a.H + c);
-    r0 += lo16(sv);
-    r1 += hi16(sv);
+    float y0, y1;
+    down_out(a, (int64_t)a.P + row, n_slices(a.SI / 16), a.tab[a.E].svh[2], c, y0, y1);
+    r0 += y0;
+    r1 += y1;
   } else if (a.shared_kind == exl3m::kSharedDense) {
     const int S = dense_splits(a.SI);
     const int64_t n = (int64_t)a.N * a.H;
@@ -384,8 +409,8 @@ namespace {
 struct MoeLayout {
   size_t total;
   size_t logits, weights, ids, sorted_row, sorted_rank, slot, run_expert, run_off, run_len, n_runs;
-  size_t yhat_gu, yw, sh_out, dsh_gu, dsh_act, dsh_dn;
-  int P, R, Imax;
+  size_t yhat_gu, act, yhat_dn, dsh_gu, dsh_act, dsh_dn;
+  int P, R, Imax, S_dn;
 };
 
 MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
@@ -412,9 +437,10 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.run_off = take(4 * (size_t)m.R);
   m.run_len = take(4 * (size_t)m.R);
   m.n_runs = take(4);
-  m.yhat_gu = take(4 * (size_t)slots * 2 * m.Imax);
-  m.yw = take(2 * (size_t)m.P * H);
-  m.sh_out = take(2 * (size_t)N * H);
+  m.yhat_gu = take(4 * (size_t)slots * 2 * moe_slices(H) * m.Imax);
+  m.act = take(2 * (size_t)slots * m.Imax);
+  m.S_dn = std::max(moe_slices(I), SI > 0 ? moe_slices(SI) : 1);
+  m.yhat_dn = take(4 * (size_t)slots * m.S_dn * H);
   m.dsh_gu = take(dense ? 4 * (size_t)2 * dense_splits(H) * N * SI : 0);
   m.dsh_act = take(dense ? 2 * (size_t)N * SI : 0);
   m.dsh_dn = take(dense ? 4 * (size_t)dense_splits(SI) * N * H : 0);
@@ -441,6 +467,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.swiglu_limit = L->cfg.swiglu_limit;
   a.shared_kind = L->shared;
   a.n_logit_blocks = (int)(((a.E + 3) / 4) * ((N + 7) / 8));
+  a.pass_rows = (int)std::min<int64_t>(N, 16);
   a.h = h;
   a.router_w = L->router_w;
   a.router_bias = L->router_bias;
@@ -457,8 +484,9 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.run_len = (int32_t *)(ws + m.run_len);
   a.n_runs = (int32_t *)(ws + m.n_runs);
   a.yhat_gu = (float *)(ws + m.yhat_gu);
-  a.yw = (uint16_t *)(ws + m.yw);
-  a.sh_out = (uint16_t *)(ws + m.sh_out);
+  a.act = (uint16_t *)(ws + m.act);
+  a.yhat_dn = (float *)(ws + m.yhat_dn);
+  a.S_dn = m.S_dn;
   a.dsh_gu = (float *)(ws + m.dsh_gu);
   a.dsh_act = (uint16_t *)(ws + m.dsh_act);
   a.dsh_dn = (float *)(ws + m.dsh_dn);
@@ -713,26 +741,32 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[1], st));
 
   const int H = layer->H, I = layer->I, SI = layer->SI;
-  // L3: routed gate/up (+ the f16 shared expert's down partials)
-  const unsigned gu_routed = (unsigned)((int64_t)m.R * 2 * (I / 128));
-  unsigned gu_blocks = gu_routed;
-  if (layer->shared == exl3m::kSharedDense) gu_blocks += (unsigned)((H / 128) * dense_splits(SI));
-  rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, gu_blocks, a, 0, (int)gu_routed, st);
+  // L3: routed gate/up
+  const int gu_sl = moe_slices(H);
+  rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, (unsigned)((int64_t)m.R * 2 * (I / 128) * gu_sl),
+                         a, 0, 0, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[2], st));
-  // L4: routed down
-  rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb, (unsigned)((int64_t)m.R * (H / 128)), a, 0,
-                         0, st);
+  // L4: routed SwiGLU activations (+ the f16 shared expert's down partials), routed down
+  rc = launch_moe_act(a, 0,
+                      layer->shared == exl3m::kSharedDense ? (H / 128) * dense_splits(SI) : 0, st);
+  if (rc) return rc;
+  rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb,
+                         (unsigned)((int64_t)m.R * (H / 128) * moe_slices(I)), a, 0, 0, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[3], st));
   // a trellis shared expert: one run of every token row through the same kernels
   if (layer->shared == exl3m::kSharedTrellis) {
-    rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, (unsigned)(2 * (SI / 128)), a, 1, 0, st);
+    rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, (unsigned)(2 * (SI / 128) * gu_sl), a, 1,
+                           0, st);
     if (rc) return rc;
-    rc = launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, (unsigned)(H / 128), a, 1, 0, st);
+    rc = launch_moe_act(a, 1, 0, st);
+    if (rc) return rc;
+    rc = launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, (unsigned)((H / 128) * moe_slices(SI)),
+                           a, 1, 0, st);
     if (rc) return rc;
   }
-  // L5: combine
+  // L6: combine
   k_moe_combine<<<(unsigned)((N * (H / 128) + 3) / 4), 256, 0, st>>>(a);
   EXL3_LAUNCHED("k_moe_combine");
   if (timed) {
@@ -777,7 +811,7 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
       const int r = rl[i];
       d.run_hist[r >= 64 ? 64 : r] += 1;
       d.shared_bytes += layer->expert_bytes[re[i]];
-      d.streamed_bytes += layer->expert_bytes[re[i]] * ((r + 3) / 4);
+      d.streamed_bytes += layer->expert_bytes[re[i]] * ((r + 15) / 16);
     }
   }
   return EXL3_OK;

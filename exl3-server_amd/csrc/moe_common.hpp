@@ -1,19 +1,22 @@
 // Shared host/device description of one MoE layer call.
 //
-// A decode call is five stream-ordered launches; every cross-workgroup dependency is
+// A decode call is six stream-ordered launches; every cross-workgroup dependency is
 // a launch boundary (no device-scope fences or completion counters):
 //   L1 k_moe_pre       router logits (+ the f16 shared expert's gate/up partials)
 //   L2 k_moe_route     top-k routing, expert-order dispatch, run table
 //                      (+ the f16 shared expert's SwiGLU)
 //   L3 k_moe_gate_up   routed gate/up, one workgroup per (run, projection, 128-column
-//                      block), full k range; raw f32 outputs per slot
-//                      (+ the f16 shared expert's down partials)
-//   L4 k_moe_down      routed down, one workgroup per (run, 128-column block): SwiGLU
-//                      and the down input Hadamard in its prologue, output Hadamard and
-//                      the routing weight in its epilogue
-//   L5 k_moe_combine   per token row: the top_k terms in rank order + shared expert
-// A trellis shared expert runs the gate/up and down kernels on one extra "run" that
-// holds every token row (two more launches).
+//                      block, k-slice); raw f32 slice partials per slot
+//   L4 k_moe_act       per (slot, 128-block): slice sums, output Hadamards, SwiGLU with
+//                      the clamp, the down input Hadamard (+ the f16 shared expert's
+//                      down partials)
+//   L5 k_moe_down      routed down, one workgroup per (run, 128-column block, k-slice);
+//                      raw f32 slice partials per slot
+//   L6 k_moe_combine   per (token row, 128-column block): per rank, the slot's down
+//                      slices summed in order, the output Hadamard (svh) and the routing
+//                      weight; the ranks summed in order; + the shared expert
+// A trellis shared expert runs the gate/up, act and down kernels on one extra "run"
+// that holds every token row (three more launches).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -45,6 +48,7 @@ struct MoeArgs {
   float routed_scaling_factor, swiglu_limit;
   int shared_kind;    // SharedKind
   int n_logit_blocks; // L1 workgroups computing router logits
+  int pass_rows;      // token rows per MFMA pass of the expert kernels (<= 16)
   // inputs
   const uint16_t *h;          // (N, H) f16
   const uint16_t *router_w;   // (E, H) f16
@@ -60,9 +64,12 @@ struct MoeArgs {
   int32_t *slot;         // (P): pair b*topk + k -> slot
   int32_t *run_expert, *run_off, *run_len;  // (R)
   int32_t *n_runs;       // (1)
-  float *yhat_gu;      // (P + N, 2, Imax): gate/up outputs before the output Hadamard
-  uint16_t *yw;        // (P, H): f16(y * w) per slot
-  uint16_t *sh_out;    // (N, H): trellis shared expert output
+  float *yhat_gu;      // (P + N, 2, S, Imax): gate/up k-slice partials (S slices of H)
+                       // before the output Hadamard
+  uint16_t *act;       // (P + N, Imax): rotated SwiGLU output per slot, MFMA k order
+  int S_dn;            // slot stride of yhat_dn in slices: max(slices(I), slices(SI))
+  float *yhat_dn;      // (P + N, S_dn, H): down k-slice partials per slot, before the
+                       // output Hadamard (slots P.. = a trellis shared expert)
   float *dsh_gu;       // (2, H/128, N, SI): f16 shared gate/up k-split partials
   uint16_t *dsh_act;   // (N, SI): f16 shared expert SwiGLU output
   float *dsh_dn;       // (SI/128, N, H): f16 shared down k-split partials

@@ -5,22 +5,27 @@
 // multiply, take/concatenate). The device-side run table drives the grid: no host
 // round trip, no member cap, and no cross-workgroup synchronisation inside a launch.
 //
-//  k_moe_gate_up  workgroup = (run, gate|up, 128-column block), 4 waves, the whole k
-//                 range: per pass of up to 2 token rows of the run, the input
-//                 Hadamard of those rows into LDS, one k chunk per wave at a time, the
-//                 chunk partials summed in chunk order -> yhat_gu (f32, per slot).
-//                 Extra workgroups compute the f16 shared expert's down partials.
-//  k_moe_down     workgroup = (run, 128-column block), 4 waves: prologue = output
-//                 Hadamards of gate/up (svh), SwiGLU with the swiglu_limit clamp (f16 op
-//                 by op) and the down projection's input Hadamard (suh), for the whole
-//                 intermediate of each row; then the QMV over it, the output Hadamard,
-//                 and f16(f32(y) * w) per slot (or the shared expert's output).
+//  k_moe_gate_up  workgroup = (run, gate|up, 128-column block, k-slice of H), 4 waves:
+//                 per pass of up to 16 token rows of the run, the input Hadamard of the
+//                 slice's part of those rows into LDS, then one n-pair (32 columns) per
+//                 wave over the slice on the MFMA core -> raw f32 slice partials in
+//                 yhat_gu. Extra workgroups compute the f16 shared expert's down
+//                 partials.
+//  k_moe_down     workgroup = (run, 128-column block), 4 waves: prologue = gate/up slice
+//                 partials summed in slice order, their output Hadamards (svh), SwiGLU
+//                 with the swiglu_limit clamp (f16 op by op) and the down projection's
+//                 input Hadamard (suh), for the whole intermediate of each row; then the
+//                 down slices, the output Hadamard, and f16(f32(y) * w) per slot (or the
+//                 shared expert's output).
 //
 // Per token row and expert the arithmetic is exl3_trellis_linear's (same input
-// Hadamard, k chunks and chunk order, output Hadamard), so a run of r rows gives the
-// same bytes as r single-row calls, and a layer call the same bytes as its experts
-// evaluated one linear at a time.
+// Hadamard, k slices and slice order, output Hadamard), and the MFMA rows of a pass
+// never mix, so a run of r rows gives the same bytes as r single-row calls, and a layer
+// call the same bytes as its experts evaluated one linear at a time.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
 
 #include "exl3_device.hpp"
 #include "exl3_internal.hpp"
@@ -53,10 +58,6 @@ __device__ __forceinline__ float swiglu1(float g, float u, float L) {
 
 constexpr int kGuThreads = 256;
 constexpr int kDnThreads = 256;
-// Token rows per pass of an expert kernel. At decode batch sizes nearly every run has
-// one or two rows; a longer run takes more passes over its (L2-resident) tile range.
-constexpr int kRowsPerPass = 2;
-static_assert(kRowsPerPass <= kMaxRowsPerPass, "row pass");
 
 struct RunInfo {
   int e, off, len;
@@ -77,215 +78,243 @@ __device__ __forceinline__ bool run_info(const MoeArgs &a, int u, int shared_mod
   return true;
 }
 
-// Waves [0, nwaves) take chunks wave, wave + nwaves, ...; each chunk partial goes to
-// part[c][r][col] in LDS.
-template <int K, int CB, int MB>
-__device__ __forceinline__ void run_chunks(const uint32_t *base, int tiles_n, int cb,
-                                           int n_chunks, int ct, int nwaves,
-                                           const uint32_t *xs, int xs_stride, float *part) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int c = wave; c < n_chunks; c += nwaves) {
-    float acc[MB][2];
-    qmv_chunk<K, CB, MB>(base, tiles_n, cb * 8 + (lane >> 3), lane & 7, c * ct, ct, xs,
-                         xs_stride, c * ct, acc);
-#pragma unroll
-    for (int r = 0; r < MB; ++r) {
-      part[(c * kRowsPerPass + r) * 128 + lane_col(lane, 0)] = acc[r][0];
-      part[(c * kRowsPerPass + r) * 128 + lane_col(lane, 1)] = acc[r][1];
-    }
-  }
-}
-
-template <int K, int CB>
-__device__ __forceinline__ void run_chunks_rt(int nr, const uint32_t *base, int tiles_n, int cb,
-                                              int n_chunks, int ct, int nwaves,
-                                              const uint32_t *xs, int xs_stride, float *part) {
-  if (nr == 1)
-    run_chunks<K, CB, 1>(base, tiles_n, cb, n_chunks, ct, nwaves, xs, xs_stride, part);
-  else
-    run_chunks<K, CB, 2>(base, tiles_n, cb, n_chunks, ct, nwaves, xs, xs_stride, part);
-}
-
-__device__ __forceinline__ float chunk_sum(const float *part, int n_chunks, int r, int col) {
-  float v = part[r * 128 + col];
-  for (int c = 1; c < n_chunks; ++c) v += part[(c * kRowsPerPass + r) * 128 + col];
-  return v;
-}
-
-
-template <int K, int CB>
-__global__ __launch_bounds__(kGuThreads) void k_moe_gate_up(MoeArgs a, int shared_mode,
-                                                            int routed_blocks) {
+// Workgroup = (run, projection, 128-column block, k-slice of H); 4 waves, wave w owns
+// n-pair 4*cb + w. Per pass of up to 16 token rows of the run: the input Hadamard of
+// the slice's 128-blocks into LDS, then one slice per wave, raw f32 partials to yhat_gu
+// (summed in slice order by k_moe_act).
+template <int K, int CB, int PD>
+__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode) {
   extern __shared__ uint32_t smem[];
-  if (!shared_mode && (int)blockIdx.x >= routed_blocks) {
-    // f16 shared expert down partials: H/128 column blocks x 256-row k splits of SI
-    static_assert(kGuThreads == 256, "dense_skinny runs on 4 waves");
-    const int b = blockIdx.x - routed_blocks;
-    const int n_cb = a.H / 128;
-    dense_skinny(a.dsh_act, a.N, a.SI, a.H, a.sh_dense[2], a.dsh_dn, b % n_cb, b / n_cb, smem);
-    return;
-  }
   const int out = shared_mode ? a.SI : a.I;
   const int n_cb = out / 128;
-  const int u = blockIdx.x / (2 * n_cb);
-  const int proj = (blockIdx.x / n_cb) % 2;
-  const int cb = blockIdx.x % n_cb;
+  const int k_tiles = a.H / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
+  int b = blockIdx.x;
+  const int sl = b % n_sl;
+  b /= n_sl;
+  const int cb = b % n_cb;
+  b /= n_cb;
+  const int proj = b & 1, u = b >> 1;
   RunInfo ri;
   if (!run_info(a, u, shared_mode, ri)) return;
   const exl3m::ExpertTab &tb = a.tab[ri.e];
   const uint32_t *base = tb.tr[proj];
   const uint16_t *suh = tb.suh[proj];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int k_tiles = a.H / 16, ct = chunk_tiles(k_tiles), n_chunks = k_tiles / ct;
-  const int xs_stride = a.H / 2;  // words per staged row
+  const int slice_k = kStepTiles * ss * 16;  // k values per slice
+  const int nblk = slice_k / 128;
+  const int xs_stride = slice_k / 2;         // words per staged row
+  const int k_base = sl * slice_k;
   uint32_t *xs = smem;
-  float *part = reinterpret_cast<float *>(smem + kRowsPerPass * xs_stride);
-  const int nblk = a.H / 128;
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + a.pass_rows * xs_stride) + wave * kSlotChunks;
 
-  for (int p0 = 0; p0 < ri.len; p0 += kRowsPerPass) {
-    const int nr = min(kRowsPerPass, ri.len - p0);
-    for (int bi = wave; bi < kRowsPerPass * nblk; bi += kGuThreads / 64) {
+  for (int p0 = 0; p0 < ri.len; p0 += a.pass_rows) {
+    const int nr = min(a.pass_rows, ri.len - p0);
+    for (int bi = wave; bi < nr * nblk; bi += kGuThreads / 64) {
       const int r = bi / nblk, blk = bi % nblk;
-      uint32_t packed = 0;
-      if (r < nr) {
-        const int row = a.sorted_row[ri.off + p0 + r];
-        const int kc = blk * 128 + 2 * lane;
-        const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
-        const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
-        float v0 = lo16(hx), v1 = hi16(hx);
-        wave_had_pre(v0, v1, lo16(sx), hi16(sx));
-        packed = pack16(v0, v1);
-      }
-      xs[r * xs_stride + blk * 64 + lane] = packed;
+      const int row = a.sorted_row[ri.off + p0 + r];
+      const int kc = k_base + blk * 128 + 2 * lane;
+      const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
+      const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
+      float v0 = lo16(hx), v1 = hi16(hx);
+      wave_had_pre(v0, v1, lo16(sx), hi16(sx));
+      stage_pair(xs + r * xs_stride, blk, lane, pack16(v0, v1));
     }
     __syncthreads();
-    run_chunks_rt<K, CB>(nr, base, out / 16, cb, n_chunks, ct, kGuThreads / 64, xs, xs_stride, part);
-    __syncthreads();
-    for (int i = threadIdx.x; i < nr * 128; i += kGuThreads) {
-      const int r = i >> 7, col = i & 127;
-      a.yhat_gu[((int64_t)(ri.off + p0 + r) * 2 + proj) * a.Imax + cb * 128 + col] =
-          chunk_sum(part, n_chunks, r, col);
+    f32x4 D0, D1;
+    qmv_slice<K, CB, PD>(base, k_tiles, out / 16, sl * kStepTiles * ss, cb * 4 + wave, ss,
+                         xs + min(lane & 15, nr - 1) * xs_stride, slot, D0, D1);
+    const int col = cb * 128 + wave * 32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = d_row(i);
+      if (r < nr) {
+        float *y = a.yhat_gu + ((int64_t)((ri.off + p0 + r) * 2 + proj) * n_sl + sl) * a.Imax + col;
+        y[d_col(0)] = D0[i];
+        y[d_col(1)] = D1[i];
+      }
     }
     __syncthreads();
   }
 }
 
-template <int K, int CB>
-__global__ __launch_bounds__(kDnThreads) void k_moe_down(MoeArgs a, int shared_mode) {
+// Workgroup = (run, 128-column block of H, k-slice of the intermediate), 4 waves, wave w
+// owns n-pair 4*cb + w. Per pass of up to 16 token rows: the rows' rotated SwiGLU
+// outputs (k_moe_act, already in the MFMA k order) for the slice into LDS, one slice
+// per wave, raw f32 partials to yhat_dn (the output Hadamard and the routing weight
+// are applied by k_moe_combine).
+template <int K, int CB, int PD>
+__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_down(MoeArgs a, int shared_mode) {
   extern __shared__ uint32_t smem[];
   const int in = shared_mode ? a.SI : a.I;
   const int n_cb = a.H / 128;
-  const int u = blockIdx.x / n_cb, cb = blockIdx.x % n_cb;
+  const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
+  int b = blockIdx.x;
+  const int sl = b % n_sl;
+  b /= n_sl;
+  const int cb = b % n_cb, u = b / n_cb;
   RunInfo ri;
   if (!run_info(a, u, shared_mode, ri)) return;
   const exl3m::ExpertTab &tb = a.tab[ri.e];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int k_tiles = in / 16, ct = chunk_tiles(k_tiles), n_chunks = k_tiles / ct;
-  const int xs_stride = in / 2;
+  const int slice_k = kStepTiles * ss * 16;
+  const int xs_stride = slice_k / 2;  // words per staged row
   uint32_t *xs = smem;
-  float *part = reinterpret_cast<float *>(smem + kRowsPerPass * xs_stride);
-  const int nblk = in / 128;
-  const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + a.pass_rows * xs_stride) + wave * kSlotChunks;
 
-  for (int p0 = 0; p0 < ri.len; p0 += kRowsPerPass) {
-    const int nr = min(kRowsPerPass, ri.len - p0);
-    // SwiGLU of the gate/up outputs and the down input Hadamard, per 128-block.
-    for (int bi = wave; bi < kRowsPerPass * nblk; bi += kDnThreads / 64) {
-      const int r = bi / nblk, blk = bi % nblk;
-      uint32_t packed = 0;
-      if (r < nr) {
-        const int64_t slot = ri.off + p0 + r;
-        const int c = blk * 128 + 2 * lane;
-        const float *yg = a.yhat_gu + (slot * 2 + 0) * a.Imax + c;
-        const float *yu = a.yhat_gu + (slot * 2 + 1) * a.Imax + c;
-        float g0 = yg[0], g1 = yg[1], u0 = yu[0], u1 = yu[1];
-        const uint32_t svg = *reinterpret_cast<const uint32_t *>(tb.svh[0] + c);
-        const uint32_t svu = *reinterpret_cast<const uint32_t *>(tb.svh[1] + c);
-        const uint32_t sud = *reinterpret_cast<const uint32_t *>(tb.suh[2] + c);
-        wave_had_post(g0, g1, lo16(svg), hi16(svg));
-        wave_had_post(u0, u1, lo16(svu), hi16(svu));
-        float a0 = swiglu1(rf16(g0), rf16(u0), L);
-        float a1 = swiglu1(rf16(g1), rf16(u1), L);
-        wave_had_pre(a0, a1, lo16(sud), hi16(sud));
-        packed = pack16(a0, a1);
-      }
-      xs[r * xs_stride + blk * 64 + lane] = packed;
+  for (int p0 = 0; p0 < ri.len; p0 += a.pass_rows) {
+    const int nr = min(a.pass_rows, ri.len - p0);
+    const int q_row = xs_stride / 4;  // 16-byte chunks per staged row
+    for (int i = threadIdx.x; i < nr * q_row; i += kDnThreads) {
+      const int r = i / q_row, q = i % q_row;
+      reinterpret_cast<uint4 *>(xs + r * xs_stride)[q] = reinterpret_cast<const uint4 *>(
+          a.act + (int64_t)(ri.off + p0 + r) * a.Imax + sl * slice_k)[q];
     }
     __syncthreads();
-    run_chunks_rt<K, CB>(nr, tb.tr[2], a.H / 16, cb, n_chunks, ct, kDnThreads / 64, xs, xs_stride,
-                         part);
-    __syncthreads();
-    const int c = cb * 128 + 2 * lane;
-    const uint32_t svd = *reinterpret_cast<const uint32_t *>(tb.svh[2] + c);
-    for (int r = wave; r < nr; r += kDnThreads / 64) {
-      float y0 = chunk_sum(part, n_chunks, r, 2 * lane);
-      float y1 = chunk_sum(part, n_chunks, r, 2 * lane + 1);
-      wave_had_post(y0, y1, lo16(svd), hi16(svd));
-      const int64_t slot = ri.off + p0 + r;
-      if (shared_mode) {
-        *reinterpret_cast<uint32_t *>(a.sh_out + (slot - a.P) * a.H + c) = pack16(y0, y1);
-      } else {
-        const int row = a.sorted_row[slot], rank = a.sorted_rank[slot];
-        const float w = a.weights[(int64_t)row * a.topk + rank];
-        *reinterpret_cast<uint32_t *>(a.yw + slot * a.H + c) = pack16(rf16(y0) * w, rf16(y1) * w);
+    f32x4 D0, D1;
+    qmv_slice<K, CB, PD>(tb.tr[2], k_tiles, a.H / 16, sl * kStepTiles * ss, cb * 4 + wave, ss,
+                         xs + min(lane & 15, nr - 1) * xs_stride, slot, D0, D1);
+    const int col = cb * 128 + wave * 32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = d_row(i);
+      if (r < nr) {
+        float *y = a.yhat_dn + ((int64_t)(ri.off + p0 + r) * a.S_dn + sl) * a.H + col;
+        y[d_col(0)] = D0[i];
+        y[d_col(1)] = D1[i];
       }
     }
     __syncthreads();
   }
+}
+
+// One wave per (slot, 128-block of the intermediate): the gate/up slice partials
+// summed in slice order, their output Hadamards (svh), SwiGLU with the swiglu_limit
+// clamp (f16 op by op), and the down projection's input Hadamard (suh) -> act (f16, in
+// the MFMA k order the down kernel stages). Routed slots come from the dispatch; in
+// shared mode the slots P..P+N-1 of the trellis shared expert. Workgroups past the
+// slots compute the f16 shared expert's down partials.
+constexpr int kActThreads = 256;
+
+__global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_mode,
+                                                         int act_blocks) {
+  extern __shared__ uint32_t smem[];
+  if ((int)blockIdx.x >= act_blocks) {
+    static_assert(kActThreads == 256, "dense_skinny runs on 4 waves");
+    const int b = blockIdx.x - act_blocks;
+    const int n_cb = a.H / 128;
+    dense_skinny(a.dsh_act, a.N, a.SI, a.H, a.sh_dense[2], a.dsh_dn, b % n_cb, b / n_cb, smem);
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int in = shared_mode ? a.SI : a.I;
+  const int nblk = in / 128;
+  const int64_t gw = (int64_t)blockIdx.x * (kActThreads / 64) + (threadIdx.x >> 6);
+  const int n_slots = shared_mode ? a.N : a.P;
+  if (gw >= (int64_t)n_slots * nblk) return;
+  const int blk = (int)(gw % nblk);
+  const int64_t slot = (shared_mode ? a.P : 0) + gw / nblk;
+  const int e = shared_mode ? a.E : a.ids[(int64_t)a.sorted_row[slot] * a.topk + a.sorted_rank[slot]];
+  const exl3m::ExpertTab &tb = a.tab[e];
+  const int gu_sl = n_slices(a.H / 16);
+  const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
+  const int c = blk * 128 + 2 * lane;
+  const float *yg = a.yhat_gu + (slot * 2 + 0) * gu_sl * a.Imax + c;
+  const float *yu = a.yhat_gu + (slot * 2 + 1) * gu_sl * a.Imax + c;
+  float g0 = yg[0], g1 = yg[1], u0 = yu[0], u1 = yu[1];
+  for (int s = 1; s < gu_sl; ++s) {
+    g0 += yg[s * a.Imax];
+    g1 += yg[s * a.Imax + 1];
+    u0 += yu[s * a.Imax];
+    u1 += yu[s * a.Imax + 1];
+  }
+  const uint32_t svg = *reinterpret_cast<const uint32_t *>(tb.svh[0] + c);
+  const uint32_t svu = *reinterpret_cast<const uint32_t *>(tb.svh[1] + c);
+  const uint32_t sud = *reinterpret_cast<const uint32_t *>(tb.suh[2] + c);
+  wave_had_post(g0, g1, lo16(svg), hi16(svg));
+  wave_had_post(u0, u1, lo16(svu), hi16(svu));
+  float a0 = swiglu1(rf16(g0), rf16(u0), L);
+  float a1 = swiglu1(rf16(g1), rf16(u1), L);
+  wave_had_pre(a0, a1, lo16(sud), hi16(sud));
+  stage_pair(reinterpret_cast<uint32_t *>(a.act + slot * a.Imax), blk, lane, pack16(a0, a1));
 }
 
 }  // namespace
 
 namespace exl3h {
 
-size_t moe_gate_up_lds(int H) {
-  const int k_tiles = H / 16;
-  return (size_t)kRowsPerPass * (H / 2) * 4 + (size_t)(k_tiles / chunk_tiles(k_tiles)) *
-                                                      kRowsPerPass * 128 * 4;
-}
-
-size_t moe_down_lds(int in) {
+// Staged activation rows of one k-slice, then one ring-word slot per wave.
+static size_t expert_lds(int in, int pass_rows, int waves) {
   const int k_tiles = in / 16;
-  return (size_t)kRowsPerPass * (in / 2) * 4 + (size_t)(k_tiles / chunk_tiles(k_tiles)) *
-                                                       kRowsPerPass * 128 * 4;
+  return (size_t)pass_rows * (kStepTiles * slice_steps(k_tiles) * 16 / 2) * 4 +
+         (size_t)waves * kSlotChunks * 16;
 }
+size_t moe_gate_up_lds(int H, int pass_rows) { return expert_lds(H, pass_rows, kGuThreads / 64); }
+size_t moe_down_lds(int in, int pass_rows) { return expert_lds(in, pass_rows, kDnThreads / 64); }
 
-template <int K, int CB>
+int moe_slices(int in) { return n_slices(in / 16); }
+
+
+template <int K, int CB, int PD>
 static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
                           int shared_mode, int routed_blocks) {
   if (which == 0) {
-    const size_t lds = std::max(moe_gate_up_lds(a.H), (size_t)4 * kDenseLdsWords);
+    const size_t lds = moe_gate_up_lds(a.H, a.pass_rows);
     static bool attr_set = false;
     if (!attr_set) {
-      EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_gate_up<K, CB>,
+      EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_gate_up<K, CB, PD>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
       attr_set = true;
     }
-    k_moe_gate_up<K, CB><<<blocks, kGuThreads, lds, st>>>(a, shared_mode, routed_blocks);
+    (void)routed_blocks;
+    k_moe_gate_up<K, CB, PD><<<blocks, kGuThreads, lds, st>>>(a, shared_mode);
   } else {
-    const size_t lds = moe_down_lds(shared_mode ? a.SI : a.I);
+    const size_t lds = moe_down_lds(shared_mode ? a.SI : a.I, a.pass_rows);
     static bool attr_set = false;
     if (!attr_set) {
-      EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_down<K, CB>,
+      EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_down<K, CB, PD>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
       attr_set = true;
     }
-    k_moe_down<K, CB><<<blocks, kDnThreads, lds, st>>>(a, shared_mode);
+    k_moe_down<K, CB, PD><<<blocks, kDnThreads, lds, st>>>(a, shared_mode);
   }
   return EXL3_OK;
 }
 
-// which: 0 = gate/up (routed_blocks = workgroups of routed runs; the rest compute the
-// f16 shared expert's down partials), 1 = down.
+template <int K, int CB>
+static exl3_status moe_pd(int pd, int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
+                          int shared_mode, int routed_blocks) {
+  if (pd == 1) return moe_go<K, CB, 1>(which, blocks, st, a, shared_mode, routed_blocks);
+  if constexpr (K <= 4) {
+    if (pd >= 4) return moe_go<K, CB, 4>(which, blocks, st, a, shared_mode, routed_blocks);
+  }
+  return moe_go<K, CB, 2>(which, blocks, st, a, shared_mode, routed_blocks);
+}
+
+// Wave steps in flight: prefetch_steps(), or EXL3_MOE_PREFETCH (1, 2 or 4; capped by
+// the slice length and, for K > 4, at 2), read once.
+static int moe_prefetch(int k_tiles, int K) {
+  static const int env = [] {
+    const char *v = std::getenv("EXL3_MOE_PREFETCH");
+    return v ? std::atoi(v) : 0;
+  }();
+  int pd = prefetch_steps(k_tiles, K);
+  if (env == 1 || env == 2 || env == 4) pd = std::min(env, slice_steps(k_tiles));
+  if (K > 4 && pd > 2) pd = 2;
+  return pd;
+}
+
+// which: 0 = gate/up, 1 = down.
 exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const MoeArgs &a,
                               int shared_mode, int routed_blocks, hipStream_t st) {
   if (blocks == 0) return EXL3_OK;
+  const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
+  const int pd = moe_prefetch(in / 16, K);
   exl3_status rc = EXL3_OK;
-#define EXL3_KC(KK)                                                                          \
-  case KK:                                                                                   \
-    if (cb == 0) rc = moe_go<KK, 0>(which, blocks, st, a, shared_mode, routed_blocks);       \
-    else if (cb == 1) rc = moe_go<KK, 1>(which, blocks, st, a, shared_mode, routed_blocks);  \
-    else rc = moe_go<KK, 2>(which, blocks, st, a, shared_mode, routed_blocks);               \
+#define EXL3_KC(KK)                                                                               \
+  case KK:                                                                                        \
+    if (cb == 0) rc = moe_pd<KK, 0>(pd, which, blocks, st, a, shared_mode, routed_blocks);       \
+    else if (cb == 1) rc = moe_pd<KK, 1>(pd, which, blocks, st, a, shared_mode, routed_blocks);  \
+    else rc = moe_pd<KK, 2>(pd, which, blocks, st, a, shared_mode, routed_blocks);               \
     break;
   switch (K) {
     EXL3_KC(1) EXL3_KC(2) EXL3_KC(3) EXL3_KC(4) EXL3_KC(5) EXL3_KC(6) EXL3_KC(7) EXL3_KC(8)
@@ -294,6 +323,26 @@ exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const M
 #undef EXL3_KC
   if (rc) return rc;
   EXL3_LAUNCHED(which == 0 ? "k_moe_gate_up" : "k_moe_down");
+  return EXL3_OK;
+}
+
+// Routed (shared_mode 0: P slots, plus the f16 shared expert's down partials when
+// dense_blocks > 0) or trellis-shared (shared_mode 1: N slots) SwiGLU activations.
+exl3_status launch_moe_act(const MoeArgs &a, int shared_mode, int dense_blocks, hipStream_t st) {
+  const int in = shared_mode ? a.SI : a.I;
+  const int64_t waves = (int64_t)(shared_mode ? a.N : a.P) * (in / 128);
+  const unsigned act_blocks = (unsigned)((waves + 3) / 4);
+  const unsigned blocks = act_blocks + (unsigned)dense_blocks;
+  if (blocks == 0) return EXL3_OK;
+  const size_t lds = dense_blocks > 0 ? (size_t)4 * kDenseLdsWords : 0;
+  static bool attr_set = false;
+  if (!attr_set) {
+    EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_act,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set = true;
+  }
+  k_moe_act<<<blocks, kActThreads, lds, st>>>(a, shared_mode, (int)act_blocks);
+  EXL3_LAUNCHED("k_moe_act");
   return EXL3_OK;
 }
 

@@ -9,6 +9,8 @@
 //                (:980, :1185) + the output Hadamard (:1186)
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "exl3_device.hpp"
 #include "exl3_internal.hpp"
 #include "qmv_core.hpp"
@@ -134,52 +136,54 @@ __global__ __launch_bounds__(256) void k_hadamard(const uint16_t *__restrict__ x
 }
 
 // ---------------------------------------------------------------------------------
-// QMV: grid (n_cb * ceil(n_chunks / 4), row passes, members); 4 waves per workgroup,
-// one k chunk per wave. Workgroup (cb, g) owns output columns [cb*128, cb*128+128) and
-// chunks [4g, 4g+4); each wave writes its chunk partial part[member][chunk][row][col].
+// QMV: grid (out/128 column blocks x k-slices, row passes, members); 4 waves per
+// workgroup, wave w owns n-pair 4*cb + w of one k-slice. The workgroup stages its
+// slice of up to 16 xhat rows into LDS in the MFMA k order and writes the slice
+// partials part[member][slice][row][col].
 // ---------------------------------------------------------------------------------
-template <int K, int CB, int MB>
+constexpr int kQmvSliceWords = kMaxSliceSteps * kStepTiles * 16 / 2;  // largest slice, words/row
+
+template <int K, int CB, int PD>
 __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_n, int in,
                                              int out, const uint16_t *__restrict__ xhat,
                                              int64_t x_member_stride, int64_t rows,
-                                             float *__restrict__ part) {
-  constexpr int kXsRow = 4 * 16 * 8;  // 4 chunks of at most 16 k-tiles, 8 words each
-  __shared__ uint32_t xs[MB * kXsRow];
-  const int k_tiles = in / 16, ct = chunk_tiles(k_tiles), n_chunks = k_tiles / ct;
+                                             int pass_rows, float *__restrict__ part) {
+  __shared__ uint32_t xs[kPassRows * kQmvSliceWords];
+  __shared__ u32x4 slots[4 * kSlotChunks];
+  const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
+  const int slice_k = kStepTiles * ss * 16, xs_stride = slice_k / 2;
   const int n_cb = out / 128;
-  const int cb = blockIdx.x % n_cb, g = blockIdx.x / n_cb;
-  const int64_t r0 = (int64_t)blockIdx.y * MB;
+  const int cb = blockIdx.x % n_cb, sl = blockIdx.x / n_cb;
+  const int64_t r0 = (int64_t)blockIdx.y * pass_rows;
+  const int nr = (int)min<int64_t>(pass_rows, rows - r0);
   const int member = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c0 = g * 4;
-  const int nc = min(4, n_chunks - c0);
-  const int kt_wg = nc * ct;
 
-  const uint16_t *xm = xhat + member * x_member_stride;
-  for (int i = threadIdx.x; i < MB * kt_wg * 8; i += 256) {
-    const int r = i / (kt_wg * 8), wd = i % (kt_wg * 8);
-    uint32_t v = 0;
-    if (r0 + r < rows) v = reinterpret_cast<const uint32_t *>(xm + (r0 + r) * in + c0 * ct * 16)[wd];
-    xs[r * kXsRow + wd] = v;
+  const uint16_t *xm = xhat + member * x_member_stride + r0 * in + sl * slice_k;
+  for (int i = threadIdx.x; i < nr * xs_stride; i += 256) {
+    const int r = i / xs_stride, w = i % xs_stride;
+    xs[r * xs_stride + (w & ~7) + xpos(w & 7)] =
+        reinterpret_cast<const uint32_t *>(xm + (int64_t)r * in)[w];
   }
   __syncthreads();
-  if (wave >= nc) return;
-  float acc[MB][2];
-  qmv_chunk<K, CB, MB>((const uint32_t *)trellis.p[member], tiles_n, cb * 8 + (lane >> 3),
-                       lane & 7, (c0 + wave) * ct, ct, xs, kXsRow, wave * ct, acc);
-  const int chunk = c0 + wave;
+  f32x4 D0, D1;
+  qmv_slice<K, CB, PD>((const uint32_t *)trellis.p[member], k_tiles, tiles_n, sl * kStepTiles * ss,
+                       cb * 4 + wave, ss, xs + min(lane & 15, nr - 1) * xs_stride,
+                       slots + wave * kSlotChunks, D0, D1);
+  float *p = part + (((int64_t)member * n_sl + sl) * rows + r0) * out + cb * 128 + wave * 32;
 #pragma unroll
-  for (int r = 0; r < MB; ++r) {
-    if (r0 + r >= rows) break;
-    float *p = part + (((int64_t)member * n_chunks + chunk) * rows + r0 + r) * out + cb * 128;
-    p[lane_col(lane, 0)] = acc[r][0];
-    p[lane_col(lane, 1)] = acc[r][1];
+  for (int i = 0; i < 4; ++i) {
+    const int r = d_row(i);
+    if (r < nr) {
+      p[(int64_t)r * out + d_col(0)] = D0[i];
+      p[(int64_t)r * out + d_col(1)] = D1[i];
+    }
   }
 }
 
-// One wave per (member, row, 128-column block): chunk partials summed in chunk order,
+// One wave per (member, row, 128-column block): slice partials summed in slice order,
 // then the raw f32 result or the output Hadamard.
-__global__ __launch_bounds__(256) void k_qmv_finalize(int n, int n_chunks, int64_t rows, int out,
+__global__ __launch_bounds__(256) void k_qmv_finalize(int n, int n_sl, int64_t rows, int out,
                                                       const float *__restrict__ part,
                                                       float *__restrict__ y32,
                                                       uint16_t *__restrict__ y16,
@@ -193,9 +197,9 @@ __global__ __launch_bounds__(256) void k_qmv_finalize(int n, int n_chunks, int64
   const int64_t row = rest % rows;
   const int member = (int)(rest / rows);
   const int c = cb * 128 + 2 * lane;
-  const float *p = part + ((int64_t)member * n_chunks * rows + row) * out + c;
+  const float *p = part + ((int64_t)member * n_sl * rows + row) * out + c;
   float v0 = p[0], v1 = p[1];
-  for (int s = 1; s < n_chunks; ++s) {
+  for (int s = 1; s < n_sl; ++s) {
     v0 += p[(int64_t)s * rows * out];
     v1 += p[(int64_t)s * rows * out + 1];
   }
@@ -257,48 +261,57 @@ exl3_status launch_hadamard(const uint16_t *x16, const float *x32, int64_t rows,
   return EXL3_OK;
 }
 
-template <int K, int CB, int MB>
+template <int K, int CB, int PD>
 static void qmv_go(dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in, int out,
-                   const uint16_t *xhat, int64_t xs, int64_t rows, float *part) {
-  k_qmv<K, CB, MB><<<grid, 256, 0, st>>>(tr, tiles_n, in, out, xhat, xs, rows, part);
+                   const uint16_t *xhat, int64_t xs, int64_t rows, int pass_rows, float *part) {
+  k_qmv<K, CB, PD><<<grid, 256, 0, st>>>(tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part);
 }
 
 template <int K, int CB>
-static void qmv_mb(int mb, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in,
-                   int out, const uint16_t *xhat, int64_t xs, int64_t rows, float *part) {
-  switch (mb) {
-    case 1: qmv_go<K, CB, 1>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
-    case 2: qmv_go<K, CB, 2>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
-    default: qmv_go<K, CB, 4>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
+static void qmv_pd(int pd, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in,
+                   int out, const uint16_t *xhat, int64_t xs, int64_t rows, int pass_rows,
+                   float *part) {
+  if (pd == 1) return qmv_go<K, CB, 1>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part);
+  if constexpr (K <= 4) {
+    if (pd >= 4) return qmv_go<K, CB, 4>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part);
   }
+  qmv_go<K, CB, 2>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part);
 }
 
 template <int K>
-static void qmv_cb(int cb, int mb, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n,
-                   int in, int out, const uint16_t *xhat, int64_t xs, int64_t rows, float *part) {
+static void qmv_cb(int cb, int pd, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n,
+                   int in, int out, const uint16_t *xhat, int64_t xs, int64_t rows, int pass_rows,
+                   float *part) {
   switch (cb) {
-    case 0: qmv_mb<K, 0>(mb, grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
-    case 1: qmv_mb<K, 1>(mb, grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
-    default: qmv_mb<K, 2>(mb, grid, st, tr, tiles_n, in, out, xhat, xs, rows, part); break;
+    case 0: qmv_pd<K, 0>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part); break;
+    case 1: qmv_pd<K, 1>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part); break;
+    default: qmv_pd<K, 2>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part); break;
   }
 }
+
+int qmv_pass_rows(int64_t rows) {
+  const exl3_tuning tn = tuning();
+  int pr = tn.rows_per_pass > 0 ? tn.rows_per_pass : kPassRows;
+  if (pr > kPassRows) pr = kPassRows;
+  return (int)std::min<int64_t>(pr, std::max<int64_t>(rows, 1));
+}
+
+int qmv_slices(int in) { return n_slices(in / 16); }
 
 exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, int n,
                        const uint16_t *xhat, int64_t x_member_stride, int64_t rows, float *part,
                        hipStream_t st) {
   const int in = shape.in_features, out = shape.out_features;
-  const KPart kp = kpart(in / 16);
-  const exl3_tuning tn = tuning();
-  int mb = tn.rows_per_pass > 0 ? tn.rows_per_pass : (rows >= 4 ? 4 : (int)rows);
-  mb = mb >= 4 ? 4 : (mb >= 2 ? 2 : 1);
-  dim3 grid((unsigned)((out / 128) * ((kp.n_chunks + 3) / 4)), (unsigned)((rows + mb - 1) / mb),
+  const int k_tiles = in / 16;
+  const int pr = qmv_pass_rows(rows);
+  dim3 grid((unsigned)((out / 128) * n_slices(k_tiles)), (unsigned)((rows + pr - 1) / pr),
             (unsigned)n);
-  const int tiles_n = out / 16;
+  const int tiles_n = out / 16, pd = prefetch_steps(k_tiles, shape.K);
   switch (shape.K) {
 #define EXL3_K(KK)                                                                        \
   case KK:                                                                                \
-    qmv_cb<KK>(shape.codebook, mb, grid, st, trellis, tiles_n, in, out, xhat,             \
-               x_member_stride, rows, part);                                              \
+    qmv_cb<KK>(shape.codebook, pd, grid, st, trellis, tiles_n, in, out, xhat,             \
+               x_member_stride, rows, pr, part);                                          \
     break;
     EXL3_K(1) EXL3_K(2) EXL3_K(3) EXL3_K(4) EXL3_K(5) EXL3_K(6) EXL3_K(7) EXL3_K(8)
 #undef EXL3_K
@@ -308,11 +321,11 @@ exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, 
   return EXL3_OK;
 }
 
-exl3_status launch_qmv_finalize(int n, int n_chunks, int64_t rows, int out, const float *part,
+exl3_status launch_qmv_finalize(int n, int n_sl, int64_t rows, int out, const float *part,
                                 float *y32, uint16_t *y16, const PtrTable &svh, hipStream_t st) {
   const int64_t waves = (int64_t)n * rows * (out / 128);
   if (waves == 0) return EXL3_OK;
-  k_qmv_finalize<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(n, n_chunks, rows, out, part, y32,
+  k_qmv_finalize<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(n, n_sl, rows, out, part, y32,
                                                               y16, svh);
   EXL3_LAUNCHED("k_qmv_finalize");
   return EXL3_OK;

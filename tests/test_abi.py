@@ -57,12 +57,15 @@ def test_path_info_and_workspace_query():
     info = _lib.PathInfo()
     d = fake_desc()
     _lib.call("exl3_trellis_path_info", C.byref(d), 8, C.byref(info))
-    assert info.staged == 0 and info.rows_per_block == 4 and info.passes == 2
-    assert info.splits == 16  # 256 k-tiles: 16 chunks of 16 k-tiles
+    # one MFMA pass serves up to 16 token rows
+    assert info.staged == 0 and info.rows_per_block == 8 and info.passes == 1
+    assert info.splits == 8  # 256 k-tiles: 8 slices of 8 wave steps of 4 k-tiles
+    _lib.call("exl3_trellis_path_info", C.byref(d), 40, C.byref(info))
+    assert info.staged == 1 and info.rows_per_block == 16 and info.passes == 3
     ws1 = L.exl3_trellis_workspace_size(C.byref(d), 1, 1)
     ws8 = L.exl3_trellis_workspace_size(C.byref(d), 8, 3)
     assert 0 < ws1 < ws8
-    assert ws1 >= 4096 * 2 + 16 * 1024 * 4  # xhat + 16 chunk planes
+    assert ws1 >= 4096 * 2 + 8 * 1024 * 4  # xhat + 8 slice planes
 
 
 def test_workspace_too_small_is_reported_before_launch():

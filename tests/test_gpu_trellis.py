@@ -125,7 +125,7 @@ def test_rows_invariance_and_row_block_knob(dev):
     for r in range(13):
         assert np.array_equal(bits(trellis_linear(w, x[r:r + 1].contiguous())), base[r:r + 1])
     try:
-        for mb in (1, 2, 4):
+        for mb in (1, 2, 4, 5, 16):
             trellis_set_tuning(rows_per_pass=mb)
             assert np.array_equal(bits(trellis_linear(w, x)), base)
     finally:
