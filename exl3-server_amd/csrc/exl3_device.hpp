@@ -152,26 +152,71 @@ __device__ __forceinline__ void lane_tile_fma(const uint32_t (&W)[K + 1],
 }
 
 // ---------------------------------------------------------------------------------
+// Lane exchange v <- v[lane ^ D] without the LDS crossbar's address arithmetic:
+// D = 1, 2: DPP quad permutes; D = 4, 8, 16: ds_swizzle xor mode (within 32 lanes);
+// D = 32: v_permlane32_swap (the two wave halves exchanged).
+// ---------------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ float xor_lanes(float v) {
+  const int iv = __builtin_bit_cast(int, v);
+  if constexpr (D == 1) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
+  } else if constexpr (D == 2) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
+  } else if constexpr (D == 4 || D == 8 || D == 16) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(iv, 0x1F | (D << 10)));
+  } else {
+    static_assert(D == 32, "xor distance");
+    // vdst' = (lo: v[i], hi: v[i - 32]), vsrc' = (lo: v[i + 32], hi: v[i])
+    const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+    const int lane = threadIdx.x & 63;
+    return __builtin_bit_cast(float, lane < 32 ? (int)r[1] : (int)r[0]);
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // 128-point Sylvester Hadamard over one wave: lane l holds elements 2l and 2l+1.
 // Stage order len = 1, 2, ..., 64 with (x[j], x[j+len]) -> (a + b, a - b), the f32
-// association of reference exl3.cpp:140-150 and trellis_gemm.cpp:387-396.
+// association of reference exl3.cpp:140-150 and trellis_gemm.cpp:387-396. NB
+// independent vectors go through the stages together, so their lane exchanges overlap.
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ void wave_fwht128(float &v0, float &v1) {
-  const int lane = threadIdx.x & 63;
-  {
-    const float a = v0, b = v1;
-    v0 = a + b;
-    v1 = a - b;
-  }
+template <int D, int NB>
+__device__ __forceinline__ void fwht_stage(float (&v0)[NB], float (&v1)[NB]) {
+  float p0[NB], p1[NB];
 #pragma unroll
-  for (int s = 0; s < 6; ++s) {
-    const int d = 1 << s;  // lane distance for element distance 2d
-    const float p0 = __shfl_xor(v0, d, 64);
-    const float p1 = __shfl_xor(v1, d, 64);
-    const bool upper = (lane & d) != 0;
-    v0 = upper ? (p0 - v0) : (v0 + p0);
-    v1 = upper ? (p1 - v1) : (v1 + p1);
+  for (int i = 0; i < NB; ++i) {
+    p0[i] = xor_lanes<D>(v0[i]);
+    p1[i] = xor_lanes<D>(v1[i]);
   }
+  const bool upper = ((threadIdx.x & 63) & D) != 0;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    v0[i] = upper ? (p0[i] - v0[i]) : (v0[i] + p0[i]);
+    v1[i] = upper ? (p1[i] - v1[i]) : (v1[i] + p1[i]);
+  }
+}
+
+template <int NB>
+__device__ __forceinline__ void wave_fwht128_n(float (&v0)[NB], float (&v1)[NB]) {
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const float a = v0[i], b = v1[i];
+    v0[i] = a + b;
+    v1[i] = a - b;
+  }
+  fwht_stage<1>(v0, v1);
+  fwht_stage<2>(v0, v1);
+  fwht_stage<4>(v0, v1);
+  fwht_stage<8>(v0, v1);
+  fwht_stage<16>(v0, v1);
+  fwht_stage<32>(v0, v1);
+}
+
+__device__ __forceinline__ void wave_fwht128(float &v0, float &v1) {
+  float a[1] = {v0}, b[1] = {v1};
+  wave_fwht128_n<1>(a, b);
+  v0 = a[0];
+  v1 = b[0];
 }
 
 // Round-trip helpers for the two sides of a trellis linear (trellis_gemm.cpp:383-399).
@@ -191,6 +236,23 @@ __device__ __forceinline__ void wave_had_post(float &v0, float &v1, float s0, fl
   wave_fwht128(v0, v1);
   v0 = f32_rounded(f32_rounded(v0 * kHadScale) * s0);
   v1 = f32_rounded(f32_rounded(v1 * kHadScale) * s1);
+}
+
+// NB independent post rotations at once (same arithmetic as wave_had_post).
+template <int NB>
+__device__ __forceinline__ void wave_had_post_n(float (&v0)[NB], float (&v1)[NB],
+                                                const float (&s0)[NB], const float (&s1)[NB]) {
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    v0[i] = (float)to_f16(v0[i]);
+    v1[i] = (float)to_f16(v1[i]);
+  }
+  wave_fwht128_n<NB>(v0, v1);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    v0[i] = f32_rounded(f32_rounded(v0[i] * kHadScale) * s0[i]);
+    v1[i] = f32_rounded(f32_rounded(v1[i] * kHadScale) * s1[i]);
+  }
 }
 
 }  // namespace exl3d

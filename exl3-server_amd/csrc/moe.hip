@@ -8,6 +8,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "exl3_device.hpp"
@@ -51,19 +52,27 @@ __global__ __launch_bounds__(256) void k_moe_pre(MoeArgs a) {
                  rem % n_cb, rem / n_cb, pre_lds);
     return;
   }
-  const int eb = (a.E + 3) / 4;
-  router_logits(a.h, a.N, a.H, a.router_w, a.E, a.logits, (blockIdx.x % eb) * 4,
-                (int64_t)(blockIdx.x / eb) * 8, pre_lds);
+  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task < ((a.E + 15) / 16) * a.logit_splits)
+    router_logits_mfma(a.h, a.N, a.H, a.router_w, a.E, a.logits, task);
 }
 
 // LDS bytes of k_moe_pre: the logits' 8 staged rows, or a dense_skinny workgroup.
-size_t pre_lds_bytes(int H) { return std::max<size_t>(16 * (size_t)H, 4 * (size_t)kDenseLdsWords); }
+size_t pre_lds_bytes(int) { return 4 * (size_t)kDenseLdsWords; }
 
 // ---------------------------------------------------------------------------------
 // Routing + dispatch, one workgroup of 16 waves (glm5_moe.cpp:16-60, 158-255).
 // ---------------------------------------------------------------------------------
 constexpr int kMaxE = 1024;
-constexpr int kJ = kMaxE / 64;
+// Route kernels are instantiated for E <= 64 * JN experts (JN 64-expert chunks per lane).
+template <typename F>
+static void with_route_chunks(int E, F &&f) {
+  if (E <= 128) f(std::integral_constant<int, 2>{});
+  else if (E <= 256) f(std::integral_constant<int, 4>{});
+  else if (E <= 320) f(std::integral_constant<int, 5>{});
+  else if (E <= 512) f(std::integral_constant<int, 8>{});
+  else f(std::integral_constant<int, 16>{});
+}
 
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);
@@ -95,25 +104,49 @@ __device__ __forceinline__ float swiglu1(float g, float u, float L) {
   return rf16(act * u);
 }
 
+// Monotone map of an f32 (not NaN) to u32: a > b  <=>  key(a) > key(b); -0 is taken as +0.
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Wave-wide max / min of a u32: DPP within rows of 16 lanes, then the 4 row values.
+__device__ __forceinline__ uint32_t row_reduce_max(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));   // lane ^ 1
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));   // lane ^ 2
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));  // half-row mirror
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false));  // row mirror
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = row_reduce_max(v);
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
+
 // L2. Workgroup 0: routing + dispatch. Workgroups 1..: the f16 shared expert's SwiGLU
 // on its gate/up partials (summed in split order, rounded to f16 like the matmul).
+template <int kJ>
 __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int32_t *id_out,
                                                     int do_dispatch) {
   __shared__ float s_buf[16][kMaxE];  // group path: scores_for_choice per wave; dispatch: counts
   __shared__ int s_keep[16][64];
   if (blockIdx.x > 0) {
-    const int64_t i = (int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x;
+    // f16 shared SwiGLU: one element pair (i, i + 1) per thread
+    const int64_t i = 2 * ((int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
     const int64_t n = (int64_t)a.N * a.SI;
     if (i >= n) return;
     const int S = dense_splits(a.H);
-    const float *pg = a.dsh_gu, *pu = a.dsh_gu + (int64_t)S * n;
-    float g = pg[i], u = pu[i];
-    for (int s = 1; s < S; ++s) {
-      g += pg[(int64_t)s * n + i];
-      u += pu[(int64_t)s * n + i];
-    }
+    const float2 g = exl3m::ordered_sum2<16>(a.dsh_gu + i, n, S);
+    const float2 u = exl3m::ordered_sum2<16>(a.dsh_gu + (int64_t)S * n + i, n, S);
     const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
-    a.dsh_act[i] = bitcast<uint16_t>(to_f16(swiglu1(rf16(g), rf16(u), L)));
+    const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(swiglu1(rf16(g.x), rf16(u.x), L))) |
+                       ((uint32_t)bitcast<uint16_t>(to_f16(swiglu1(rf16(g.y), rf16(u.y), L))) << 16);
+    *reinterpret_cast<uint32_t *>(a.dsh_act + i) = o;
     return;
   }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -122,17 +155,40 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
   const int tg = a.topk_group > 0 ? min(a.topk_group, ng) : 1;
   const int gsize = E / ng;
 
+  const int jn = (E + 63) / 64;
+  const int S = a.logit_splits;  // 0: plain logits (N, E); else S partials in (N, E, 8)
   for (int b = wave; b < a.N; b += 16) {
+    // all logit partial and bias loads first (clamped addresses, so no branches split
+    // them), then the split sums in split order, the sigmoid and the biased score
     float sc[kJ], sfc[kJ];
-    const float *lg = a.logits + (int64_t)b * E;
+    float4 lp[kJ][2];
+    float bias[kJ];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
+      const int e = min(lane + 64 * j, E - 1);
+      if (S == 0) {
+        lp[j][0].x = a.logits[(int64_t)b * E + e];
+      } else {
+        const float4 *q = reinterpret_cast<const float4 *>(a.logits + ((int64_t)b * E + e) * kLogitSlots);
+        lp[j][0] = q[0];
+        lp[j][1] = q[1];
+      }
+      bias[j] = a.router_bias[e];
+    }
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const float v[8] = {lp[j][0].x, lp[j][0].y, lp[j][0].z, lp[j][0].w,
+                          lp[j][1].x, lp[j][1].y, lp[j][1].z, lp[j][1].w};
+      float lg = v[0];
+#pragma unroll
+      for (int s = 1; s < 8; ++s)
+        if (s < S) lg += v[s];
       const int e = lane + 64 * j;
       sc[j] = 0.0f;
       sfc[j] = -INFINITY;
       if (e < E) {
-        sc[j] = 1.0f / (1.0f + expf(-lg[e]));
-        sfc[j] = sc[j] + a.router_bias[e];
+        sc[j] = 1.0f / (1.0f + expf(-lg));
+        sfc[j] = sc[j] + bias[j];
       }
     }
     if (ng > 1) {
@@ -181,39 +237,36 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
         if (e < E && !s_keep[wave][e / gsize]) sfc[j] = -INFINITY;
       }
     }
+    // top_k by repeated wave argmax: largest sfc, ties to the lower expert id
     uint32_t taken = 0;
     float denom = 0.0f;
     float my_w = 0.0f;
     int my_id = 0;
     for (int k = 0; k < K; ++k) {
-      float bv = -INFINITY;
-      int bi = 1 << 30;
-      float bs = 0.0f;
+      uint32_t bkey = 0;
+      int bj = 0;
+      float bsc = 0.0f;
 #pragma unroll
       for (int j = 0; j < kJ; ++j) {
         const int e = lane + 64 * j;
-        if (e < E && !((taken >> j) & 1u) && better(sfc[j], e, bv, bi)) {
-          bv = sfc[j];
-          bi = e;
-          bs = sc[j];
+        if (j < jn && e < E && !((taken >> j) & 1u)) {
+          const uint32_t key = order_key(sfc[j]);
+          if (key > bkey) {
+            bkey = key;
+            bj = j;
+            bsc = sc[j];
+          }
         }
       }
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) {
-        const float ov = __shfl_xor(bv, d, 64);
-        const int oi = __shfl_xor(bi, d, 64);
-        const float os = __shfl_xor(bs, d, 64);
-        if (better(ov, oi, bv, bi)) {
-          bv = ov;
-          bi = oi;
-          bs = os;
-        }
-      }
-      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+      const uint32_t mkey = wave_max_u32(bkey);
+      const uint32_t ewin = wave_min_u32(bkey == mkey && bkey != 0 ? (uint32_t)(lane + 64 * bj) : 0xFFFFFFFFu);
+      const int wl = (int)(ewin & 63u);
+      const float bs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bsc), wl));
+      if (lane == wl) taken |= 1u << (ewin >> 6);
       denom += bs;
       if (lane == k) {
         my_w = bs;
-        my_id = bi;
+        my_id = (int)ewin;
       }
     }
     if (lane < K) {
@@ -300,6 +353,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       const int pos = cnt[wave * kMaxE + e] + __builtin_popcountll(m & lanes_below());
       a.sorted_row[pos] = p / K;
       a.sorted_rank[pos] = p % K;
+      a.slot_e[pos] = e;
       a.slot[p] = pos;
     }
     __builtin_amdgcn_wave_barrier();
@@ -319,16 +373,15 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
 // f16(f32(y) * w_k); routed = f16(sum of those f16 terms in rank order), then
 // out = f16(routed + shared).
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ void down_out(const MoeArgs &a, int64_t slot, int n_sl,
-                                         const uint16_t *svh, int c, float &y0, float &y1) {
-  const float *p = a.yhat_dn + slot * a.S_dn * a.H + c;
-  y0 = p[0];
-  y1 = p[1];
-  for (int s = 1; s < n_sl; ++s) {
-    y0 += p[(int64_t)s * a.H];
-    y1 += p[(int64_t)s * a.H + 1];
-  }
-  const uint32_t sv = *reinterpret_cast<const uint32_t *>(svh + c);
+// Ranks are taken 8 at a time: their slot/expert/weight, their down slice partials and
+// svh words are all loaded before the first output Hadamard, so a row costs a few
+// memory round trips instead of a few per rank.
+constexpr int kCombineBatch = 8;
+constexpr int kCombineSlices = 4;  // down slices loaded at once (intermediate <= 2048)
+
+__device__ __forceinline__ void down_out(float2 y, uint32_t sv, float &y0, float &y1) {
+  y0 = y.x;
+  y1 = y.y;
   wave_had_post(y0, y1, lo16(sv), hi16(sv));
   y0 = rf16(y0);
   y1 = rf16(y1);
@@ -342,34 +395,87 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   const int row = (int)(gw / n_cb), cb = (int)(gw % n_cb);
   const int c = cb * 128 + 2 * lane;
   const int n_sl = n_slices(a.I / 16);
+  const int64_t plane = a.H;  // floats between slice planes of one slot
   float r0 = 0.0f, r1 = 0.0f;
-  for (int k = 0; k < a.topk; ++k) {
-    const int64_t pk = (int64_t)row * a.topk + k;
-    const int e = a.ids[pk];
-    const float w = a.weights[pk];
-    float y0, y1;
-    down_out(a, a.slot[pk], n_sl, a.tab[e].svh[2], c, y0, y1);
-    r0 += rf16(y0 * w);
-    r1 += rf16(y1 * w);
+  for (int k0 = 0; k0 < a.topk; k0 += kCombineBatch) {
+    const int nk = min(kCombineBatch, a.topk - k0);
+    // three rounds of loads, each for all ranks of the batch at once (rank indices
+    // clamped, so no branch separates them): pair -> slot/expert/weight -> the expert's
+    // svh pointer -> svh words and the slot's down slice partials
+    int64_t slot[kCombineBatch];
+    int e[kCombineBatch];
+    float w[kCombineBatch];
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) {
+      const int64_t pk = (int64_t)row * a.topk + min(k0 + j, a.topk - 1);
+      slot[j] = a.slot[pk];
+      e[j] = a.ids[pk];
+      w[j] = a.weights[pk];
+    }
+    const uint16_t *svp[kCombineBatch];
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) svp[j] = a.tab[e[j]].svh[2];
+    uint32_t sv[kCombineBatch];
+    float2 y[kCombineBatch];
+    if (n_sl <= kCombineSlices) {
+      float2 part[kCombineBatch][kCombineSlices];
+#pragma unroll
+      for (int j = 0; j < kCombineBatch; ++j) {
+        sv[j] = *reinterpret_cast<const uint32_t *>(svp[j] + c);
+#pragma unroll
+        for (int q = 0; q < kCombineSlices; ++q)
+          part[j][q] = *reinterpret_cast<const float2 *>(
+              a.yhat_dn + (slot[j] * a.S_dn + min(q, n_sl - 1)) * plane + c);
+      }
+#pragma unroll
+      for (int j = 0; j < kCombineBatch; ++j) {
+        y[j] = part[j][0];
+#pragma unroll
+        for (int q = 1; q < kCombineSlices; ++q)
+          if (q < n_sl) {
+            y[j].x += part[j][q].x;
+            y[j].y += part[j][q].y;
+          }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kCombineBatch; ++j) {
+        sv[j] = *reinterpret_cast<const uint32_t *>(svp[j] + c);
+        y[j] = exl3m::ordered_sum2<4>(a.yhat_dn + slot[j] * a.S_dn * plane + c, plane, n_sl);
+      }
+    }
+    float v0[kCombineBatch], v1[kCombineBatch], s0[kCombineBatch], s1[kCombineBatch];
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) {
+      v0[j] = y[j].x;
+      v1[j] = y[j].y;
+      s0[j] = lo16(sv[j]);
+      s1[j] = hi16(sv[j]);
+    }
+    wave_had_post_n<kCombineBatch>(v0, v1, s0, s1);
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) {
+      if (j < nk) {
+        r0 += rf16(rf16(v0[j]) * w[j]);
+        r1 += rf16(rf16(v1[j]) * w[j]);
+      }
+    }
   }
   r0 = rf16(r0);
   r1 = rf16(r1);
   if (a.shared_kind == exl3m::kSharedTrellis) {
+    const int64_t slot = (int64_t)a.P + row;
+    const float2 ys = exl3m::ordered_sum2<4>(a.yhat_dn + slot * a.S_dn * plane + c, plane,
+                                                          n_slices(a.SI / 16));
     float y0, y1;
-    down_out(a, (int64_t)a.P + row, n_slices(a.SI / 16), a.tab[a.E].svh[2], c, y0, y1);
+    down_out(ys, *reinterpret_cast<const uint32_t *>(a.tab[a.E].svh[2] + c), y0, y1);
     r0 += y0;
     r1 += y1;
   } else if (a.shared_kind == exl3m::kSharedDense) {
-    const int S = dense_splits(a.SI);
-    const int64_t n = (int64_t)a.N * a.H;
-    const float *p = a.dsh_dn + (int64_t)row * a.H + c;
-    float s0 = p[0], s1 = p[1];
-    for (int s = 1; s < S; ++s) {
-      s0 += p[(int64_t)s * n];
-      s1 += p[(int64_t)s * n + 1];
-    }
-    r0 += rf16(s0);
-    r1 += rf16(s1);
+    const float2 sd = exl3m::ordered_sum2<4>(a.dsh_dn + (int64_t)row * a.H + c, (int64_t)a.N * a.H,
+                                              dense_splits(a.SI));
+    r0 += rf16(sd.x);
+    r1 += rf16(sd.y);
   }
   const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(r0)) |
                      ((uint32_t)bitcast<uint16_t>(to_f16(r1)) << 16);
@@ -408,7 +514,8 @@ namespace {
 
 struct MoeLayout {
   size_t total;
-  size_t logits, weights, ids, sorted_row, sorted_rank, slot, run_expert, run_off, run_len, n_runs;
+  size_t logits, weights, ids, sorted_row, sorted_rank, slot_e, slot, run_expert, run_off, run_len,
+      n_runs;
   size_t yhat_gu, act, yhat_dn, dsh_gu, dsh_act, dsh_dn;
   int P, R, Imax, S_dn;
 };
@@ -427,11 +534,12 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   };
   const int64_t slots = m.P + N;
   const bool dense = L->shared == exl3m::kSharedDense;
-  m.logits = take(4 * N * E);
+  m.logits = take(4 * N * E * kLogitSlots);
   m.weights = take(4 * (size_t)m.P);
   m.ids = take(4 * (size_t)m.P);
   m.sorted_row = take(4 * (size_t)slots);
   m.sorted_rank = take(4 * (size_t)slots);
+  m.slot_e = take(4 * (size_t)slots);
   m.slot = take(4 * (size_t)m.P);
   m.run_expert = take(4 * (size_t)m.R);
   m.run_off = take(4 * (size_t)m.R);
@@ -466,7 +574,8 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.routed_scaling_factor = L->cfg.routed_scaling_factor;
   a.swiglu_limit = L->cfg.swiglu_limit;
   a.shared_kind = L->shared;
-  a.n_logit_blocks = (int)(((a.E + 3) / 4) * ((N + 7) / 8));
+  a.logit_splits = logit_splits(a.H);
+  a.n_logit_blocks = (((a.E + 15) / 16) * a.logit_splits + 3) / 4;
   a.pass_rows = (int)std::min<int64_t>(N, 16);
   a.h = h;
   a.router_w = L->router_w;
@@ -478,6 +587,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.ids = (int32_t *)(ws + m.ids);
   a.sorted_row = (int32_t *)(ws + m.sorted_row);
   a.sorted_rank = (int32_t *)(ws + m.sorted_rank);
+  a.slot_e = (int32_t *)(ws + m.slot_e);
   a.slot = (int32_t *)(ws + m.slot);
   a.run_expert = (int32_t *)(ws + m.run_expert);
   a.run_off = (int32_t *)(ws + m.run_off);
@@ -520,8 +630,10 @@ exl3_status launch_logits_route(exl3_moe_layer_s *L, const MoeArgs &a, float *w_
   });
   k_moe_pre<<<pre_blocks, 256, lds, st>>>(a);
   EXL3_LAUNCHED("k_moe_pre");
-  const int fin_blocks = dense ? (int)(((int64_t)a.N * a.SI + 1023) / 1024) : 0;
-  k_moe_route<<<1 + fin_blocks, 1024, 0, st>>>(a, w_out, id_out, do_dispatch);
+  const int fin_blocks = dense ? (int)(((int64_t)a.N * a.SI / 2 + 1023) / 1024) : 0;
+  with_route_chunks(a.E, [&](auto jn) {
+    k_moe_route<decltype(jn)::value><<<1 + fin_blocks, 1024, 0, st>>>(a, w_out, id_out, do_dispatch);
+  });
   EXL3_LAUNCHED("k_moe_route");
   return EXL3_OK;
 }
@@ -547,7 +659,8 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
   const int K = cfg->num_experts_per_tok;
   if (H <= 0 || H % 128 || I <= 0 || I % 128)
     return fail(EXL3_ERR_INVALID, "hidden and intermediate sizes must be positive multiples of 128");
-  if (H > 8192) return fail(EXL3_ERR_UNSUPPORTED, "hidden_size must be <= 8192");
+  if (H > 8192 || I > 8192)
+    return fail(EXL3_ERR_UNSUPPORTED, "hidden and intermediate sizes must be <= 8192");
   if (E <= 0 || E > 1024) return fail(EXL3_ERR_UNSUPPORTED, "n_routed_experts must be in 1..1024");
   if (K <= 0 || K > E || K > 64) return fail(EXL3_ERR_INVALID, "num_experts_per_tok must be in 1..min(E, 64)");
   const int ng = cfg->n_group > 1 ? cfg->n_group : 1;
@@ -587,6 +700,10 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
     if (SI <= 0 || SI % 128) {
       delete L;
       return fail(EXL3_ERR_INVALID, "shared intermediate must be a positive multiple of 128");
+    }
+    if (SI > 8192) {
+      delete L;
+      return fail(EXL3_ERR_UNSUPPORTED, "shared intermediate size must be <= 8192");
     }
     for (int j = 0; j < 3; ++j) {
       exl3_status rc = check_linear(sh[j], j == 2 ? SI : H, j == 2 ? H : SI, "shared expert");
@@ -713,7 +830,10 @@ exl3_status exl3_moe_topk_route(const float *logits, const float *bias, int64_t 
   a.routed_scaling_factor = cfg->routed_scaling_factor;
   a.router_bias = bias;
   a.logits = const_cast<float *>(logits);
-  k_moe_route<<<1, 1024, 0, stream_of(stream)>>>(a, weights, ids, 0);
+  a.logit_splits = 0;  // plain (N, E) logits
+  with_route_chunks(E, [&](auto jn) {
+    k_moe_route<decltype(jn)::value><<<1, 1024, 0, stream_of(stream)>>>(a, weights, ids, 0);
+  });
   EXL3_LAUNCHED("k_moe_route");
   return EXL3_OK;
 }

@@ -48,6 +48,7 @@ struct MoeArgs {
   float routed_scaling_factor, swiglu_limit;
   int shared_kind;    // SharedKind
   int n_logit_blocks; // L1 workgroups computing router logits
+  int logit_splits;   // k-split partials per logit (0: plain logits given by the caller)
   int pass_rows;      // token rows per MFMA pass of the expert kernels (<= 16)
   // inputs
   const uint16_t *h;          // (N, H) f16
@@ -56,11 +57,12 @@ struct MoeArgs {
   const ExpertTab *tab;       // E (+1) entries
   const uint16_t *sh_dense[3];  // f16 shared expert weights (in, out) when dense
   // workspace
-  float *logits;       // (N, E)
+  float *logits;       // (N, E, 8): router logit k-split partials, or (N, E) plain logits
   float *weights;      // (N, topk)
   int32_t *ids;        // (N, topk)
   int32_t *sorted_row;   // (P + N): slot -> token row; slots P.. are the shared rows
   int32_t *sorted_rank;  // (P + N): slot -> rank
+  int32_t *slot_e;       // (P): slot -> expert
   int32_t *slot;         // (P): pair b*topk + k -> slot
   int32_t *run_expert, *run_off, *run_len;  // (R)
   int32_t *n_runs;       // (1)
@@ -75,5 +77,30 @@ struct MoeArgs {
   float *dsh_dn;       // (SI/128, N, H): f16 shared down k-split partials
   uint16_t *out;       // (N, H)
 };
+
+// Column pair (c, c + 1) summed over n partial planes in plane order, p[0] + p[1] + ...
+// (plane stride `stride` floats). MAXN planes are loaded at a time, unconditionally
+// (plane indices clamped to n - 1, the extra values unused), before their adds: with
+// no branch between them the loads are all in flight together. p: 8-byte aligned.
+template <int MAXN>
+__device__ __forceinline__ float2 ordered_sum2(const float *p, int64_t stride, int n) {
+  float2 acc = make_float2(0.0f, 0.0f);
+  for (int s0 = 0; s0 < n; s0 += MAXN) {
+    float2 v[MAXN];
+#pragma unroll
+    for (int s = 0; s < MAXN; ++s)
+      v[s] = *reinterpret_cast<const float2 *>(p + (int64_t)min(s0 + s, n - 1) * stride);
+#pragma unroll
+    for (int s = 0; s < MAXN; ++s) {
+      if (s0 + s == 0) {
+        acc = v[0];
+      } else if (s0 + s < n) {
+        acc.x += v[s].x;
+        acc.y += v[s].y;
+      }
+    }
+  }
+  return acc;
+}
 
 }  // namespace exl3m

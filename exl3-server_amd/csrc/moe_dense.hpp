@@ -52,28 +52,25 @@ __device__ __forceinline__ void dense_skinny(const uint16_t *__restrict__ x, int
     for (int r = 0; r < kDenseRows; ++r)
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[r][c] = 0.0f;
-#pragma unroll 1
-    for (int i0 = 0; i0 < 32; i0 += 8) {
-      u32x2 wv[8];
+    // all 32 of this lane's weight loads are issued before the first product
+    u32x2 wv[32];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = k0 + wave * 64 + 2 * (i0 + i) + q;
-        wv[i] = k < in ? __builtin_nontemporal_load(
-                             reinterpret_cast<const u32x2 *>(W + (int64_t)k * out + col))
-                       : u32x2{0u, 0u};
-      }
+    for (int i = 0; i < 32; ++i) {
+      // rows past `in` load row in - 1: their staged x is zero, so they add nothing
+      const int k = min(k0 + wave * 64 + 2 * i + q, in - 1);
+      wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(W + (int64_t)k * out + col));
+    }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int kk = wave * 64 + 2 * (i0 + i) + q;  // k row inside this split
+    for (int i = 0; i < 32; ++i) {
+      const int kk = wave * 64 + 2 * i + q;  // k row inside this split
 #pragma unroll
-        for (int r = 0; r < kDenseRows; ++r) {
-          const uint32_t xw = xs[r * (kDenseKR / 2) + (kk >> 1)];
-          const float xv = q ? hi16f(xw) : lo16f(xw);
-          acc[r][0] = fmaf(xv, lo16f(wv[i].x), acc[r][0]);
-          acc[r][1] = fmaf(xv, hi16f(wv[i].x), acc[r][1]);
-          acc[r][2] = fmaf(xv, lo16f(wv[i].y), acc[r][2]);
-          acc[r][3] = fmaf(xv, hi16f(wv[i].y), acc[r][3]);
-        }
+      for (int r = 0; r < kDenseRows; ++r) {
+        const uint32_t xw = xs[r * (kDenseKR / 2) + (kk >> 1)];
+        const float xv = q ? hi16f(xw) : lo16f(xw);
+        acc[r][0] = fmaf(xv, lo16f(wv[i].x), acc[r][0]);
+        acc[r][1] = fmaf(xv, hi16f(wv[i].x), acc[r][1]);
+        acc[r][2] = fmaf(xv, lo16f(wv[i].y), acc[r][2]);
+        acc[r][3] = fmaf(xv, hi16f(wv[i].y), acc[r][3]);
       }
     }
 #pragma unroll
@@ -99,64 +96,54 @@ __device__ __forceinline__ void dense_skinny(const uint16_t *__restrict__ x, int
   }
 }
 
-// Router logits for 4 experts per wave-group: one wave per expert e, logits[t][e] =
-// sum_k f32(h[t][k]) * f32(router_w[e][k]) for token rows [r0, r0 + 8). Lane l holds
-// the 16-byte chunks k = 8l + 512j of the expert's row (all loads issued at once); the
-// lane partials are reduced with an xor-shuffle tree. xs: LDS, 8 rows x H/2 words.
-__device__ __forceinline__ void router_logits(const uint16_t *__restrict__ h, int64_t rows,
-                                              int H, const uint16_t *__restrict__ rw, int E,
-                                              float *__restrict__ logits, int e0, int64_t r0,
-                                              uint32_t *xs) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nr = (int)min<int64_t>(8, rows - r0);
-  for (int i0 = threadIdx.x; i0 < H; i0 += 4 * 256) {  // 8 rows x H/8 16-byte chunks
-    uint4 v[4];
+// Router logits on the matrix cores (glm5_moe.cpp:127-128): logits = f32(h) f32(W)^T
+// with W = router_w (E, H) f16 as on disk. Products of f16 values are exact in f32,
+// so only the summation order differs from a scalar f32 dot product. H is cut into
+// logit_splits(H) <= 8 equal k splits; a wave task is (16 experts, one split): lane l
+// loads 8 consecutive k of expert 16nb + l%16 (the B operand, k-group l/16) for 16
+// 32-k steps at a time, the matching h values of 16 token rows (the A operand), and
+// accumulates the 16x16x32 MFMAs in step order. The split partials go to
+// part[(row * E + e) * kLogitSlots + s], summed in split order by the router.
+typedef _Float16 f16x8_ __attribute__((ext_vector_type(8)));
+typedef float f32x4_ __attribute__((ext_vector_type(4)));
+
+constexpr int kLogitSlots = 8;      // partial slots per logit (splits <= 8)
+constexpr int kLogitChunk = 16;     // 32-k MFMA steps whose operands are loaded at once
+
+__host__ __device__ constexpr int logit_splits(int H) {
+  return (H / 128) % 8 == 0 ? 8 : ((H / 128) % 4 == 0 ? 4 : ((H / 128) % 2 == 0 ? 2 : 1));
+}
+
+__device__ __forceinline__ void router_logits_mfma(const uint16_t *__restrict__ h, int64_t rows,
+                                                   int H, const uint16_t *__restrict__ rw, int E,
+                                                   float *__restrict__ part, int task) {
+  const int lane = threadIdx.x & 63;
+  const int S = logit_splits(H), sk = H / S, nsteps = sk / 32;
+  const int nb = task / S, sp = task % S;
+  const int e = nb * 16 + (lane & 15), g = lane >> 4;
+  const int ec = e < E ? e : E - 1;  // out-of-range columns load a valid row, never stored
+  const int k0 = sp * sk + 8 * g;
+  for (int64_t r0 = 0; r0 < rows; r0 += 16) {
+    const int64_t row = r0 + (lane & 15);
+    const int64_t rc = row < rows ? row : rows - 1;
+    f32x4_ D = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int q0 = 0; q0 < nsteps; q0 += kLogitChunk) {
+      f16x8_ A[kLogitChunk], B[kLogitChunk];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = i0 + 256 * u, r = i / (H / 8), c8 = i % (H / 8);
-      v[u] = (i < H && r < nr) ? *reinterpret_cast<const uint4 *>(h + (r0 + r) * H + 8 * c8)
-                               : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (i0 + 256 * u < H) reinterpret_cast<uint4 *>(xs)[i0 + 256 * u] = v[u];
-  }
-  __syncthreads();
-  const int e = e0 + wave;
-  if (e >= E) return;
-  constexpr int kMaxChunks = 16;  // H <= 8192
-  const int nch = (H + 511) / 512;
-  uint4 wv[kMaxChunks];
-#pragma unroll
-  for (int j = 0; j < kMaxChunks; ++j) {
-    wv[j] = make_uint4(0u, 0u, 0u, 0u);  // lanes past H contribute zero
-    if (j < nch && 512 * j + 8 * lane < H)
-      wv[j] = *reinterpret_cast<const uint4 *>(rw + (int64_t)e * H + 512 * j + 8 * lane);
-  }
-  float acc[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kMaxChunks; ++j) {
-    const uint32_t w4[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-    if (j >= nch || 512 * j + 8 * lane >= H) continue;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const uint4 x4 = *reinterpret_cast<const uint4 *>(xs + r * (H / 2) + 256 * j + 4 * lane);
-      const uint32_t xv[4] = {x4.x, x4.y, x4.z, x4.w};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        acc[r] = fmaf(lo16f(xv[c]), lo16f(w4[c]), acc[r]);
-        acc[r] = fmaf(hi16f(xv[c]), hi16f(w4[c]), acc[r]);
+      for (int q = 0; q < kLogitChunk; ++q) {
+        const int k = k0 + 32 * min(q0 + q, nsteps - 1);
+        B[q] = *reinterpret_cast<const f16x8_ *>(rw + (int64_t)ec * H + k);
+        A[q] = *reinterpret_cast<const f16x8_ *>(h + rc * H + k);
       }
+#pragma unroll
+      for (int q = 0; q < kLogitChunk; ++q)
+        if (q0 + q < nsteps) D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[q], B[q], D, 0, 0, 0);
     }
-  }
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    float v = acc[r];
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    if (lane == 0 && r < nr) logits[(r0 + r) * E + e] = v;
+    for (int i = 0; i < 4; ++i) {
+      const int64_t rr = r0 + 4 * g + i;
+      if (rr < rows && e < E) part[(rr * E + e) * kLogitSlots + sp] = D[i];
+    }
   }
 }
 

@@ -213,27 +213,45 @@ __global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_m
   if (gw >= (int64_t)n_slots * nblk) return;
   const int blk = (int)(gw % nblk);
   const int64_t slot = (shared_mode ? a.P : 0) + gw / nblk;
-  const int e = shared_mode ? a.E : a.ids[(int64_t)a.sorted_row[slot] * a.topk + a.sorted_rank[slot]];
-  const exl3m::ExpertTab &tb = a.tab[e];
   const int gu_sl = n_slices(a.H / 16);
   const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
   const int c = blk * 128 + 2 * lane;
-  const float *yg = a.yhat_gu + (slot * 2 + 0) * gu_sl * a.Imax + c;
-  const float *yu = a.yhat_gu + (slot * 2 + 1) * gu_sl * a.Imax + c;
-  float g0 = yg[0], g1 = yg[1], u0 = yu[0], u1 = yu[1];
-  for (int s = 1; s < gu_sl; ++s) {
-    g0 += yg[s * a.Imax];
-    g1 += yg[s * a.Imax + 1];
-    u0 += yu[s * a.Imax];
-    u1 += yu[s * a.Imax + 1];
+  // the slice partials are loaded while the expert's scale pointers are fetched
+  constexpr int kMaxSl = 8;
+  const float *pg = a.yhat_gu + (slot * 2 + 0) * gu_sl * a.Imax + c;
+  const float *pu = a.yhat_gu + (slot * 2 + 1) * gu_sl * a.Imax + c;
+  float2 vg[kMaxSl], vu[kMaxSl];
+#pragma unroll
+  for (int q = 0; q < kMaxSl; ++q) {
+    const int64_t o = (int64_t)min(q, gu_sl - 1) * a.Imax;
+    vg[q] = *reinterpret_cast<const float2 *>(pg + o);
+    vu[q] = *reinterpret_cast<const float2 *>(pu + o);
   }
-  const uint32_t svg = *reinterpret_cast<const uint32_t *>(tb.svh[0] + c);
-  const uint32_t svu = *reinterpret_cast<const uint32_t *>(tb.svh[1] + c);
-  const uint32_t sud = *reinterpret_cast<const uint32_t *>(tb.suh[2] + c);
-  wave_had_post(g0, g1, lo16(svg), hi16(svg));
-  wave_had_post(u0, u1, lo16(svu), hi16(svu));
-  float a0 = swiglu1(rf16(g0), rf16(u0), L);
-  float a1 = swiglu1(rf16(g1), rf16(u1), L);
+  const int e = shared_mode ? a.E : a.slot_e[slot];
+  const exl3m::ExpertTab &tb = a.tab[e];
+  const uint16_t *svg_p = tb.svh[0], *svu_p = tb.svh[1], *sud_p = tb.suh[2];
+  const uint32_t svg = *reinterpret_cast<const uint32_t *>(svg_p + c);
+  const uint32_t svu = *reinterpret_cast<const uint32_t *>(svu_p + c);
+  const uint32_t sud = *reinterpret_cast<const uint32_t *>(sud_p + c);
+  float2 gs = vg[0], us = vu[0];
+#pragma unroll
+  for (int q = 1; q < kMaxSl; ++q)
+    if (q < gu_sl) {
+      gs.x += vg[q].x;
+      gs.y += vg[q].y;
+      us.x += vu[q].x;
+      us.y += vu[q].y;
+    }
+  if (gu_sl > kMaxSl) {
+    gs = exl3m::ordered_sum2<8>(pg, a.Imax, gu_sl);
+    us = exl3m::ordered_sum2<8>(pu, a.Imax, gu_sl);
+  }
+  float g0 = gs.x, g1 = gs.y, u0 = us.x, u1 = us.y;
+  float y0[2] = {g0, u0}, y1[2] = {g1, u1};
+  const float s0[2] = {lo16(svg), lo16(svu)}, s1[2] = {hi16(svg), hi16(svu)};
+  wave_had_post_n<2>(y0, y1, s0, s1);
+  float a0 = swiglu1(rf16(y0[0]), rf16(y0[1]), L);
+  float a1 = swiglu1(rf16(y1[0]), rf16(y1[1]), L);
   wave_had_pre(a0, a1, lo16(sud), hi16(sud));
   stage_pair(reinterpret_cast<uint32_t *>(a.act + slot * a.Imax), blk, lane, pack16(a0, a1));
 }
