@@ -35,6 +35,7 @@ __device__ __forceinline__ float lo16(uint32_t v) { return (float)bitcast<f16>((
 __device__ __forceinline__ float hi16(uint32_t v) { return (float)bitcast<f16>((uint16_t)(v >> 16)); }
 __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 
+
 // ---------------------------------------------------------------------------------
 // L1. Router logits: logits[t][e] = sum_k f32(h[t][k]) * f32(router_w[e][k])
 // (glm5_moe.cpp:127-128): one wave per expert, 8 token rows per workgroup staged in
@@ -43,22 +44,10 @@ __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 // 256-row k split).
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_moe_pre(MoeArgs a) {
-  extern __shared__ uint32_t pre_lds[];
-  if ((int)blockIdx.x >= a.n_logit_blocks) {
-    const int b = blockIdx.x - a.n_logit_blocks;
-    const int n_cb = a.SI / 128, S = dense_splits(a.H);
-    const int proj = b / (n_cb * S), rem = b % (n_cb * S);
-    dense_skinny(a.h, a.N, a.H, a.SI, a.sh_dense[proj], a.dsh_gu + (int64_t)proj * S * a.N * a.SI,
-                 rem % n_cb, rem / n_cb, pre_lds);
-    return;
-  }
   const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (task < ((a.E + 15) / 16) * a.logit_splits)
     router_logits_mfma(a.h, a.N, a.H, a.router_w, a.E, a.logits, task);
 }
-
-// LDS bytes of k_moe_pre: the logits' 8 staged rows, or a dense_skinny workgroup.
-size_t pre_lds_bytes(int) { return 4 * (size_t)kDenseLdsWords; }
 
 // ---------------------------------------------------------------------------------
 // Routing + dispatch, one workgroup of 16 waves (glm5_moe.cpp:16-60, 158-255).
@@ -94,15 +83,6 @@ __device__ __forceinline__ uint64_t lanes_below() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-__device__ __forceinline__ float swiglu1(float g, float u, float L) {
-  if (L > 0.0f) {
-    g = fminf(g, L);
-    u = fminf(fmaxf(u, -L), L);
-  }
-  const float sg = rf16(1.0f / (1.0f + expf(-g)));
-  const float act = rf16(g * sg);
-  return rf16(act * u);
-}
 
 // Monotone map of an f32 (not NaN) to u32: a > b  <=>  key(a) > key(b); -0 is taken as +0.
 __device__ __forceinline__ uint32_t order_key(float v) {
@@ -128,27 +108,12 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
 
-// L2. Workgroup 0: routing + dispatch. Workgroups 1..: the f16 shared expert's SwiGLU
-// on its gate/up partials (summed in split order, rounded to f16 like the matmul).
+// L2. Routing + dispatch, one workgroup.
 template <int kJ>
 __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int32_t *id_out,
                                                     int do_dispatch) {
   __shared__ float s_buf[16][kMaxE];  // group path: scores_for_choice per wave; dispatch: counts
   __shared__ int s_keep[16][64];
-  if (blockIdx.x > 0) {
-    // f16 shared SwiGLU: one element pair (i, i + 1) per thread
-    const int64_t i = 2 * ((int64_t)(blockIdx.x - 1) * 1024 + threadIdx.x);
-    const int64_t n = (int64_t)a.N * a.SI;
-    if (i >= n) return;
-    const int S = dense_splits(a.H);
-    const float2 g = exl3m::ordered_sum2<16>(a.dsh_gu + i, n, S);
-    const float2 u = exl3m::ordered_sum2<16>(a.dsh_gu + (int64_t)S * n + i, n, S);
-    const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
-    const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(swiglu1(rf16(g.x), rf16(u.x), L))) |
-                       ((uint32_t)bitcast<uint16_t>(to_f16(swiglu1(rf16(g.y), rf16(u.y), L))) << 16);
-    *reinterpret_cast<uint32_t *>(a.dsh_act + i) = o;
-    return;
-  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = a.E, K = a.topk;
   const int ng = a.n_group > 1 ? a.n_group : 1;
@@ -615,24 +580,14 @@ exl3_status check_linear(const exl3_linear_desc &d, int in, int out, const char 
   return EXL3_OK;
 }
 
-// L1 + L2: logits (+ f16 shared gate/up partials), then routing/dispatch (+ f16
-// shared SwiGLU). w_out / id_out receive the routing.
+// L1 + L2: logits, then routing/dispatch. w_out / id_out receive the routing.
 exl3_status launch_logits_route(exl3_moe_layer_s *L, const MoeArgs &a, float *w_out, int32_t *id_out,
                                 int do_dispatch, hipStream_t st) {
-  const bool dense = do_dispatch && L->shared == exl3m::kSharedDense;
-  int pre_blocks = a.n_logit_blocks;
-  if (dense) pre_blocks += 2 * (a.SI / 128) * dense_splits(a.H);
-  const size_t lds = pre_lds_bytes(a.H);
-  static std::once_flag attr_once;
-  std::call_once(attr_once, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_moe_pre),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  });
-  k_moe_pre<<<pre_blocks, 256, lds, st>>>(a);
+  (void)L;
+  k_moe_pre<<<a.n_logit_blocks, 256, 0, st>>>(a);
   EXL3_LAUNCHED("k_moe_pre");
-  const int fin_blocks = dense ? (int)(((int64_t)a.N * a.SI / 2 + 1023) / 1024) : 0;
   with_route_chunks(a.E, [&](auto jn) {
-    k_moe_route<decltype(jn)::value><<<1 + fin_blocks, 1024, 0, st>>>(a, w_out, id_out, do_dispatch);
+    k_moe_route<decltype(jn)::value><<<1, 1024, 0, st>>>(a, w_out, id_out, do_dispatch);
   });
   EXL3_LAUNCHED("k_moe_route");
   return EXL3_OK;
@@ -779,6 +734,7 @@ exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer) {
   if (!layer) return EXL3_OK;
   if (layer->ev_made)
     for (int i = 0; i < 5; ++i) (void)hipEventDestroy(layer->ev[i]);
+
   if (layer->tab_dev) {
     hipError_t e = hipFree(layer->tab_dev);
     if (e != hipSuccess) {
@@ -861,18 +817,20 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[1], st));
 
   const int H = layer->H, I = layer->I, SI = layer->SI;
-  // L3: routed gate/up
+  // L3: routed gate/up (+ the f16 shared expert's gate/up partials)
+  const bool dense_sh = layer->shared == exl3m::kSharedDense;
   const int gu_sl = moe_slices(H);
   rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, (unsigned)((int64_t)m.R * 2 * (I / 128) * gu_sl),
-                         a, 0, 0, st);
+                         a, 0, dense_sh ? shared_gate_up_blocks(H, SI) : 0, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[2], st));
-  // L4: routed SwiGLU activations (+ the f16 shared expert's down partials), routed down
-  rc = launch_moe_act(a, 0,
-                      layer->shared == exl3m::kSharedDense ? (H / 128) * dense_splits(SI) : 0, st);
+  // L4: routed SwiGLU activations (+ the f16 shared expert's SwiGLU), L5: routed down
+  // (+ the f16 shared expert's down partials)
+  rc = launch_moe_act(a, 0, dense_sh ? shared_swiglu_blocks(N, SI) : 0, st);
   if (rc) return rc;
   rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb,
-                         (unsigned)((int64_t)m.R * (H / 128) * moe_slices(I)), a, 0, 0, st);
+                         (unsigned)((int64_t)m.R * (H / 128) * moe_slices(I)), a, 0,
+                         dense_sh ? shared_down_blocks(H, SI) : 0, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[3], st));
   // a trellis shared expert: one run of every token row through the same kernels

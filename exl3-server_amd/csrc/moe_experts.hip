@@ -45,16 +45,6 @@ __device__ __forceinline__ uint32_t pack16(float a, float b) {
 }
 __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 
-// silu(min(g, L)) * clamp(u, -L, L), every MLX f16 op rounded (glm5_moe.cpp:369-371).
-__device__ __forceinline__ float swiglu1(float g, float u, float L) {
-  if (L > 0.0f) {
-    g = fminf(g, L);
-    u = fminf(fmaxf(u, -L), L);
-  }
-  const float sg = rf16(1.0f / (1.0f + expf(-g)));
-  const float act = rf16(g * sg);
-  return rf16(act * u);
-}
 
 constexpr int kGuThreads = 256;
 constexpr int kDnThreads = 256;
@@ -83,12 +73,16 @@ __device__ __forceinline__ bool run_info(const MoeArgs &a, int u, int shared_mod
 // the slice's 128-blocks into LDS, then one slice per wave, raw f32 partials to yhat_gu
 // (summed in slice order by k_moe_act).
 template <int K, int CB, int PD>
-__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode) {
+__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
+  if ((int)blockIdx.x < dense_blocks) {
+    shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu, blockIdx.x, smem);
+    return;
+  }
   const int out = shared_mode ? a.SI : a.I;
   const int n_cb = out / 128;
   const int k_tiles = a.H / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
-  int b = blockIdx.x;
+  int b = blockIdx.x - dense_blocks;
   const int sl = b % n_sl;
   b /= n_sl;
   const int cb = b % n_cb;
@@ -143,12 +137,16 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8
 // per wave, raw f32 partials to yhat_dn (the output Hadamard and the routing weight
 // are applied by k_moe_combine).
 template <int K, int CB, int PD>
-__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_down(MoeArgs a, int shared_mode) {
+__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
+  if ((int)blockIdx.x < dense_blocks) {
+    shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn, blockIdx.x, smem);
+    return;
+  }
   const int in = shared_mode ? a.SI : a.I;
   const int n_cb = a.H / 128;
   const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
-  int b = blockIdx.x;
+  int b = blockIdx.x - dense_blocks;
   const int sl = b % n_sl;
   b /= n_sl;
   const int cb = b % n_cb, u = b / n_cb;
@@ -191,24 +189,18 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8
 // summed in slice order, their output Hadamards (svh), SwiGLU with the swiglu_limit
 // clamp (f16 op by op), and the down projection's input Hadamard (suh) -> act (f16, in
 // the MFMA k order the down kernel stages). Routed slots come from the dispatch; in
-// shared mode the slots P..P+N-1 of the trellis shared expert. Workgroups past the
-// slots compute the f16 shared expert's down partials.
+// shared mode the slots P..P+N-1 of the trellis shared expert.
 constexpr int kActThreads = 256;
 
-__global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_mode,
-                                                         int act_blocks) {
-  extern __shared__ uint32_t smem[];
-  if ((int)blockIdx.x >= act_blocks) {
-    static_assert(kActThreads == 256, "dense_skinny runs on 4 waves");
-    const int b = blockIdx.x - act_blocks;
-    const int n_cb = a.H / 128;
-    dense_skinny(a.dsh_act, a.N, a.SI, a.H, a.sh_dense[2], a.dsh_dn, b % n_cb, b / n_cb, smem);
+__global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_mode, int dense_blocks) {
+  if ((int)blockIdx.x < dense_blocks) {
+    shared_swiglu_block(a.dsh_gu, a.N, a.H, a.SI, a.swiglu_limit, a.dsh_act, blockIdx.x);
     return;
   }
   const int lane = threadIdx.x & 63;
   const int in = shared_mode ? a.SI : a.I;
   const int nblk = in / 128;
-  const int64_t gw = (int64_t)blockIdx.x * (kActThreads / 64) + (threadIdx.x >> 6);
+  const int64_t gw = (int64_t)(blockIdx.x - dense_blocks) * (kActThreads / 64) + (threadIdx.x >> 6);
   const int n_slots = shared_mode ? a.N : a.P;
   if (gw >= (int64_t)n_slots * nblk) return;
   const int blk = (int)(gw % nblk);
@@ -274,38 +266,38 @@ int moe_slices(int in) { return n_slices(in / 16); }
 
 template <int K, int CB, int PD>
 static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
-                          int shared_mode, int routed_blocks) {
+                          int shared_mode, int dense_blocks) {
+  const size_t dense_lds = dense_blocks > 0 ? (size_t)4 * kDenseLdsWords : 0;
   if (which == 0) {
-    const size_t lds = moe_gate_up_lds(a.H, a.pass_rows);
+    const size_t lds = std::max(moe_gate_up_lds(a.H, a.pass_rows), dense_lds);
     static bool attr_set = false;
     if (!attr_set) {
       EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_gate_up<K, CB, PD>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
       attr_set = true;
     }
-    (void)routed_blocks;
-    k_moe_gate_up<K, CB, PD><<<blocks, kGuThreads, lds, st>>>(a, shared_mode);
+    k_moe_gate_up<K, CB, PD><<<blocks, kGuThreads, lds, st>>>(a, shared_mode, dense_blocks);
   } else {
-    const size_t lds = moe_down_lds(shared_mode ? a.SI : a.I, a.pass_rows);
+    const size_t lds = std::max(moe_down_lds(shared_mode ? a.SI : a.I, a.pass_rows), dense_lds);
     static bool attr_set = false;
     if (!attr_set) {
       EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_down<K, CB, PD>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
       attr_set = true;
     }
-    k_moe_down<K, CB, PD><<<blocks, kDnThreads, lds, st>>>(a, shared_mode);
+    k_moe_down<K, CB, PD><<<blocks, kDnThreads, lds, st>>>(a, shared_mode, dense_blocks);
   }
   return EXL3_OK;
 }
 
 template <int K, int CB>
 static exl3_status moe_pd(int pd, int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
-                          int shared_mode, int routed_blocks) {
-  if (pd == 1) return moe_go<K, CB, 1>(which, blocks, st, a, shared_mode, routed_blocks);
+                          int shared_mode, int dense_blocks) {
+  if (pd == 1) return moe_go<K, CB, 1>(which, blocks, st, a, shared_mode, dense_blocks);
   if constexpr (K <= 4) {
-    if (pd >= 4) return moe_go<K, CB, 4>(which, blocks, st, a, shared_mode, routed_blocks);
+    if (pd >= 4) return moe_go<K, CB, 4>(which, blocks, st, a, shared_mode, dense_blocks);
   }
-  return moe_go<K, CB, 2>(which, blocks, st, a, shared_mode, routed_blocks);
+  return moe_go<K, CB, 2>(which, blocks, st, a, shared_mode, dense_blocks);
 }
 
 // Wave steps in flight: prefetch_steps(), or EXL3_MOE_PREFETCH (1, 2 or 4; capped by
@@ -321,18 +313,20 @@ static int moe_prefetch(int k_tiles, int K) {
   return pd;
 }
 
-// which: 0 = gate/up, 1 = down.
+// which: 0 = gate/up, 1 = down; `blocks` routed workgroups after `dense_blocks` f16
+// shared-expert workgroups.
 exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const MoeArgs &a,
-                              int shared_mode, int routed_blocks, hipStream_t st) {
+                              int shared_mode, int dense_blocks, hipStream_t st) {
+  blocks += (unsigned)dense_blocks;
   if (blocks == 0) return EXL3_OK;
   const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
   const int pd = moe_prefetch(in / 16, K);
   exl3_status rc = EXL3_OK;
 #define EXL3_KC(KK)                                                                               \
   case KK:                                                                                        \
-    if (cb == 0) rc = moe_pd<KK, 0>(pd, which, blocks, st, a, shared_mode, routed_blocks);       \
-    else if (cb == 1) rc = moe_pd<KK, 1>(pd, which, blocks, st, a, shared_mode, routed_blocks);  \
-    else rc = moe_pd<KK, 2>(pd, which, blocks, st, a, shared_mode, routed_blocks);               \
+    if (cb == 0) rc = moe_pd<KK, 0>(pd, which, blocks, st, a, shared_mode, dense_blocks);        \
+    else if (cb == 1) rc = moe_pd<KK, 1>(pd, which, blocks, st, a, shared_mode, dense_blocks);   \
+    else rc = moe_pd<KK, 2>(pd, which, blocks, st, a, shared_mode, dense_blocks);                \
     break;
   switch (K) {
     EXL3_KC(1) EXL3_KC(2) EXL3_KC(3) EXL3_KC(4) EXL3_KC(5) EXL3_KC(6) EXL3_KC(7) EXL3_KC(8)
@@ -344,22 +338,14 @@ exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const M
   return EXL3_OK;
 }
 
-// Routed (shared_mode 0: P slots, plus the f16 shared expert's down partials when
-// dense_blocks > 0) or trellis-shared (shared_mode 1: N slots) SwiGLU activations.
+// Routed (shared_mode 0: P slots) or trellis-shared (shared_mode 1: N slots) SwiGLU
+// activations, after `dense_blocks` workgroups of the f16 shared expert's SwiGLU.
 exl3_status launch_moe_act(const MoeArgs &a, int shared_mode, int dense_blocks, hipStream_t st) {
   const int in = shared_mode ? a.SI : a.I;
   const int64_t waves = (int64_t)(shared_mode ? a.N : a.P) * (in / 128);
-  const unsigned act_blocks = (unsigned)((waves + 3) / 4);
-  const unsigned blocks = act_blocks + (unsigned)dense_blocks;
+  const unsigned blocks = (unsigned)((waves + 3) / 4) + (unsigned)dense_blocks;
   if (blocks == 0) return EXL3_OK;
-  const size_t lds = dense_blocks > 0 ? (size_t)4 * kDenseLdsWords : 0;
-  static bool attr_set = false;
-  if (!attr_set) {
-    EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_act,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_set = true;
-  }
-  k_moe_act<<<blocks, kActThreads, lds, st>>>(a, shared_mode, (int)act_blocks);
+  k_moe_act<<<blocks, kActThreads, 0, st>>>(a, shared_mode, dense_blocks);
   EXL3_LAUNCHED("k_moe_act");
   return EXL3_OK;
 }
