@@ -38,15 +38,13 @@ __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 
 // ---------------------------------------------------------------------------------
 // L1. Router logits: logits[t][e] = sum_k f32(h[t][k]) * f32(router_w[e][k])
-// (glm5_moe.cpp:127-128): one wave per expert, 8 token rows per workgroup staged in
-// LDS; f16*f16 products are exact in f32. Workgroups past the logits compute the f16
-// shared expert's gate/up k-split partials (one per projection, 128-column block and
-// 256-row k split).
+// (glm5_moe.cpp:127-128) on the matrix cores, one wave task per (16 experts, k split);
+// f16*f16 products are exact in f32. The router sums the split partials in order.
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_moe_pre(MoeArgs a) {
   const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (task < ((a.E + 15) / 16) * a.logit_splits)
-    router_logits_mfma(a.h, a.N, a.H, a.router_w, a.E, a.logits, task);
+    dense_mfma<kLogitChunk>(a.h, a.N, a.H, a.router_w, a.E, a.logits, task);
 }
 
 // ---------------------------------------------------------------------------------
@@ -134,7 +132,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       if (S == 0) {
         lp[j][0].x = a.logits[(int64_t)b * E + e];
       } else {
-        const float4 *q = reinterpret_cast<const float4 *>(a.logits + ((int64_t)b * E + e) * kLogitSlots);
+        const float4 *q = reinterpret_cast<const float4 *>(a.logits + ((int64_t)b * E + e) * kDenseSlots);
         lp[j][0] = q[0];
         lp[j][1] = q[1];
       }
@@ -437,14 +435,28 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     r0 += y0;
     r1 += y1;
   } else if (a.shared_kind == exl3m::kSharedDense) {
-    const float2 sd = exl3m::ordered_sum2<4>(a.dsh_dn + (int64_t)row * a.H + c, (int64_t)a.N * a.H,
-                                              dense_splits(a.SI));
-    r0 += rf16(sd.x);
-    r1 += rf16(sd.y);
+    const float *pd = a.dsh_dn + ((int64_t)row * a.H + c) * kDenseSlots;
+    const int S = dense_mfma_splits(a.SI);
+    r0 += rf16(dense_slots_sum(pd, S));
+    r1 += rf16(dense_slots_sum(pd + kDenseSlots, S));
   }
   const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(r0)) |
                      ((uint32_t)bitcast<uint16_t>(to_f16(r1)) << 16);
   *reinterpret_cast<uint32_t *>(a.out + (int64_t)row * a.H + c) = o;
+}
+
+// (in, out) f16 -> (out, in) f16 through a 64x64 LDS tile per workgroup (256 threads);
+// used once per f16 shared expert projection when the layer is created.
+__global__ __launch_bounds__(256) void k_transpose_f16(const uint16_t *__restrict__ src, int in,
+                                                       int out, uint16_t *__restrict__ dst) {
+  __shared__ uint16_t t[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4)
+    if (r0 + r < in && c0 + tx < out) t[r][tx] = src[(int64_t)(r0 + r) * out + c0 + tx];
+  __syncthreads();
+  for (int c = ty; c < 64; c += 4)
+    if (c0 + c < out && r0 + tx < in) dst[(int64_t)(c0 + c) * in + r0 + tx] = t[tx][c];
 }
 
 }  // namespace
@@ -460,7 +472,8 @@ struct exl3_moe_layer_s {
   int gu_K, gu_cb, dn_K, dn_cb;
   int shared;        // exl3m::SharedKind
   int SI, sh_K, sh_cb, sh_dn_K, sh_dn_cb;
-  const uint16_t *sh_dense[3];
+  const uint16_t *sh_dense[3];  // the caller's (in, out) f16 weights
+  uint16_t *sh_dense_t[3];      // layer-owned (out, in) copies read by the kernels
   const uint16_t *router_w;
   const float *router_bias;
   ExpertTab *tab_dev;  // E + 1 entries
@@ -499,7 +512,7 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   };
   const int64_t slots = m.P + N;
   const bool dense = L->shared == exl3m::kSharedDense;
-  m.logits = take(4 * N * E * kLogitSlots);
+  m.logits = take(4 * N * E * kDenseSlots);
   m.weights = take(4 * (size_t)m.P);
   m.ids = take(4 * (size_t)m.P);
   m.sorted_row = take(4 * (size_t)slots);
@@ -514,9 +527,9 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.act = take(2 * (size_t)slots * m.Imax);
   m.S_dn = std::max(moe_slices(I), SI > 0 ? moe_slices(SI) : 1);
   m.yhat_dn = take(4 * (size_t)slots * m.S_dn * H);
-  m.dsh_gu = take(dense ? 4 * (size_t)2 * dense_splits(H) * N * SI : 0);
+  m.dsh_gu = take(dense ? 4 * (size_t)2 * N * SI * kDenseSlots : 0);
   m.dsh_act = take(dense ? 2 * (size_t)N * SI : 0);
-  m.dsh_dn = take(dense ? 4 * (size_t)dense_splits(SI) * N * H : 0);
+  m.dsh_dn = take(dense ? 4 * (size_t)N * H * kDenseSlots : 0);
   m.total = o;
   return m;
 }
@@ -539,14 +552,14 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.routed_scaling_factor = L->cfg.routed_scaling_factor;
   a.swiglu_limit = L->cfg.swiglu_limit;
   a.shared_kind = L->shared;
-  a.logit_splits = logit_splits(a.H);
-  a.n_logit_blocks = (((a.E + 15) / 16) * a.logit_splits + 3) / 4;
+  a.logit_splits = dense_mfma_splits(a.H);
+  a.n_logit_blocks = (dense_mfma_tasks(a.H, a.E) + 3) / 4;
   a.pass_rows = (int)std::min<int64_t>(N, 16);
   a.h = h;
   a.router_w = L->router_w;
   a.router_bias = L->router_bias;
   a.tab = L->tab_dev;
-  for (int j = 0; j < 3; ++j) a.sh_dense[j] = L->sh_dense[j];
+  for (int j = 0; j < 3; ++j) a.sh_dense[j] = L->sh_dense_t[j];
   a.logits = (float *)(ws + m.logits);
   a.weights = (float *)(ws + m.weights);
   a.ids = (int32_t *)(ws + m.ids);
@@ -684,6 +697,28 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
     L->sh_dn_K = quant ? sh[2].tw.K : 0;
     L->sh_dn_cb = quant ? sh[2].tw.codebook : 0;
     for (int j = 0; j < 3; ++j) L->sh_dense[j] = sh[j].dense;
+    if (dense) {
+      const size_t n = (size_t)H * SI;
+      hipError_t e0 = hipMalloc(&L->sh_dense_t[0], 3 * n * sizeof(uint16_t));
+      if (e0 != hipSuccess) {
+        delete L;
+        return hip_check(e0, "hipMalloc(shared expert copy)");
+      }
+      L->sh_dense_t[1] = L->sh_dense_t[0] + n;
+      L->sh_dense_t[2] = L->sh_dense_t[0] + 2 * n;
+      for (int j = 0; j < 3 && e0 == hipSuccess; ++j) {
+        const int in = j == 2 ? SI : H, out_f = j == 2 ? H : SI;
+        k_transpose_f16<<<dim3((out_f + 63) / 64, (in + 63) / 64), 256, 0, 0>>>(
+            sh[j].dense, in, out_f, L->sh_dense_t[j]);
+        e0 = hipGetLastError();
+      }
+      if (e0 == hipSuccess) e0 = hipStreamSynchronize(0);
+      if (e0 != hipSuccess) {
+        (void)hipFree(L->sh_dense_t[0]);
+        delete L;
+        return hip_check(e0, "transpose(shared expert)");
+      }
+    }
   }
   std::vector<ExpertTab> tab((size_t)E + 1);
   L->expert_bytes.resize(E);
@@ -712,12 +747,14 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
   }
   hipError_t e1 = hipMalloc(&L->tab_dev, sizeof(ExpertTab) * tab.size());
   if (e1 != hipSuccess) {
+    if (L->sh_dense_t[0]) (void)hipFree(L->sh_dense_t[0]);
     delete L;
     return hip_check(e1, "hipMalloc(expert table)");
   }
   e1 = hipMemcpy(L->tab_dev, tab.data(), sizeof(ExpertTab) * tab.size(), hipMemcpyHostToDevice);
   if (e1 != hipSuccess) {
     (void)hipFree(L->tab_dev);
+    if (L->sh_dense_t[0]) (void)hipFree(L->sh_dense_t[0]);
     delete L;
     return hip_check(e1, "hipMemcpy(expert table)");
   }
@@ -735,6 +772,14 @@ exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer) {
   if (layer->ev_made)
     for (int i = 0; i < 5; ++i) (void)hipEventDestroy(layer->ev[i]);
 
+  if (layer->sh_dense_t[0]) {
+    hipError_t e = hipFree(layer->sh_dense_t[0]);
+    if (e != hipSuccess) {
+      (void)hipFree(layer->tab_dev);
+      delete layer;
+      return hip_check(e, "hipFree(shared expert copy)");
+    }
+  }
   if (layer->tab_dev) {
     hipError_t e = hipFree(layer->tab_dev);
     if (e != hipSuccess) {

@@ -2,16 +2,15 @@
 //
 // A decode call is six stream-ordered launches; every cross-workgroup dependency is
 // a launch boundary (no device-scope fences or completion counters):
-//   L1 k_moe_pre       router logits (+ the f16 shared expert's gate/up partials)
-//   L2 k_moe_route     top-k routing, expert-order dispatch, run table
-//                      (+ the f16 shared expert's SwiGLU)
+//   L1 k_moe_pre       router logits on the matrix cores (k-split partials)
+//   L2 k_moe_route     split sums, top-k routing, expert-order dispatch, run table
 //   L3 k_moe_gate_up   routed gate/up, one workgroup per (run, projection, 128-column
 //                      block, k-slice); raw f32 slice partials per slot
+//                      (+ the f16 shared expert's gate/up partials, extra workgroups)
 //   L4 k_moe_act       per (slot, 128-block): slice sums, output Hadamards, SwiGLU with
-//                      the clamp, the down input Hadamard (+ the f16 shared expert's
-//                      down partials)
+//                      the clamp, the down input Hadamard (+ the f16 shared SwiGLU)
 //   L5 k_moe_down      routed down, one workgroup per (run, 128-column block, k-slice);
-//                      raw f32 slice partials per slot
+//                      raw f32 slice partials per slot (+ the f16 shared down partials)
 //   L6 k_moe_combine   per (token row, 128-column block): per rank, the slot's down
 //                      slices summed in order, the output Hadamard (svh) and the routing
 //                      weight; the ranks summed in order; + the shared expert
@@ -55,7 +54,7 @@ struct MoeArgs {
   const uint16_t *router_w;   // (E, H) f16
   const float *router_bias;   // (E) f32
   const ExpertTab *tab;       // E (+1) entries
-  const uint16_t *sh_dense[3];  // f16 shared expert weights (in, out) when dense
+  const uint16_t *sh_dense[3];  // f16 shared expert weights, transposed (out, in), when dense
   // workspace
   float *logits;       // (N, E, 8): router logit k-split partials, or (N, E) plain logits
   float *weights;      // (N, topk)
@@ -72,9 +71,9 @@ struct MoeArgs {
   int S_dn;            // slot stride of yhat_dn in slices: max(slices(I), slices(SI))
   float *yhat_dn;      // (P + N, S_dn, H): down k-slice partials per slot, before the
                        // output Hadamard (slots P.. = a trellis shared expert)
-  float *dsh_gu;       // (2, H/128, N, SI): f16 shared gate/up k-split partials
+  float *dsh_gu;       // (2, N, SI, 8): f16 shared gate/up k-split partials
   uint16_t *dsh_act;   // (N, SI): f16 shared expert SwiGLU output
-  float *dsh_dn;       // (SI/128, N, H): f16 shared down k-split partials
+  float *dsh_dn;       // (N, H, 8): f16 shared down k-split partials
   uint16_t *out;       // (N, H)
 };
 

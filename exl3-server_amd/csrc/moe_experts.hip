@@ -76,7 +76,7 @@ template <int K, int CB, int PD>
 __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
   if ((int)blockIdx.x < dense_blocks) {
-    shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu, blockIdx.x, smem);
+    shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu, blockIdx.x);
     return;
   }
   const int out = shared_mode ? a.SI : a.I;
@@ -140,7 +140,7 @@ template <int K, int CB, int PD>
 __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
   if ((int)blockIdx.x < dense_blocks) {
-    shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn, blockIdx.x, smem);
+    shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn, blockIdx.x);
     return;
   }
   const int in = shared_mode ? a.SI : a.I;
@@ -267,9 +267,8 @@ int moe_slices(int in) { return n_slices(in / 16); }
 template <int K, int CB, int PD>
 static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
                           int shared_mode, int dense_blocks) {
-  const size_t dense_lds = dense_blocks > 0 ? (size_t)4 * kDenseLdsWords : 0;
   if (which == 0) {
-    const size_t lds = std::max(moe_gate_up_lds(a.H, a.pass_rows), dense_lds);
+    const size_t lds = moe_gate_up_lds(a.H, a.pass_rows);
     static bool attr_set = false;
     if (!attr_set) {
       EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_gate_up<K, CB, PD>,
@@ -278,7 +277,7 @@ static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeA
     }
     k_moe_gate_up<K, CB, PD><<<blocks, kGuThreads, lds, st>>>(a, shared_mode, dense_blocks);
   } else {
-    const size_t lds = std::max(moe_down_lds(shared_mode ? a.SI : a.I, a.pass_rows), dense_lds);
+    const size_t lds = moe_down_lds(shared_mode ? a.SI : a.I, a.pass_rows);
     static bool attr_set = false;
     if (!attr_set) {
       EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_down<K, CB, PD>,
