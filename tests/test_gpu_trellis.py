@@ -157,3 +157,18 @@ def test_many_members_beyond_one_launch(dev):
     g = bits(trellis_linear_group(ws, x))
     one = bits(trellis_linear(w, x))
     assert all(np.array_equal(g[i], one) for i in range(130))
+
+
+@pytest.mark.parametrize("K,cb", [(1, 0), (4, 1), (5, 2), (8, 1)])
+def test_dword_aligned_base(dev, K, cb):
+    # the ABI requires a 4-byte-aligned base (not 16): a copy at base + 4 bytes gives
+    # the same bits as the 256-byte-aligned original
+    w, *_ = make(dev, 1024, 512, K, cb, f"al.{K}.{cb}")
+    big = torch.empty(w.packed.numel() + 2, dtype=torch.int16, device=dev)
+    big[2:].copy_(w.packed.reshape(-1))
+    moved = TrellisWeight(big[2:].view(w.packed.shape), w.suh, w.svh, w.in_features,
+                          w.out_features, K, cb)
+    assert moved.packed.data_ptr() % 16 == 4
+    x = x_f16(dev, 3, 1024, f"al.x.{K}")
+    assert np.array_equal(bits(trellis_linear(moved, x)), bits(trellis_linear(w, x)))
+    assert np.array_equal(bits(trellis_decode(moved)), bits(trellis_decode(w)))
