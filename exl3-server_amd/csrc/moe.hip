@@ -21,10 +21,11 @@
 using namespace exl3d;
 using exl3m::ExpertTab;
 using exl3m::MoeArgs;
+using exl3m::kLongRows;
 
 namespace exl3h {
-exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const MoeArgs &a,
-                              int shared_mode, int routed_blocks, hipStream_t st);
+exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeArgs &a,
+                              int shared_mode, bool dense, hipStream_t st);
 int moe_slices(int in);
 exl3_status launch_moe_act(const MoeArgs &a, int shared_mode, int dense_blocks, hipStream_t st);
 }
@@ -42,8 +43,8 @@ __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 // f16*f16 products are exact in f32. The router sums the split partials in order.
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_moe_pre(MoeArgs a) {
-  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (task < ((a.E + 15) / 16) * a.logit_splits)
+  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task < dense_mfma_tasks(a.N, a.H, a.E))
     dense_mfma<kLogitChunk>(a.h, a.N, a.H, a.router_w, a.E, a.logits, task);
 }
 
@@ -265,29 +266,35 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
   int tot = 0;
   if (t < E)
     for (int w = 0; w < 16; ++w) tot += cnt[w * kMaxE + t];
-  // block exclusive scan of tot and of (tot > 0)
-  int v = tot, f = tot > 0 ? 1 : 0;
+  // block exclusive scans of tot, of (tot > 0) and of the run's pass count (passes of
+  // at most kLongRows rows, the work units of the long-run expert kernels)
+  const int npass = (tot + kLongRows - 1) / kLongRows;
+  int v = tot, f = tot > 0 ? 1 : 0, g = npass;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    const int ov = __shfl_up(v, d, 64), of = __shfl_up(f, d, 64);
+    const int ov = __shfl_up(v, d, 64), of = __shfl_up(f, d, 64), og = __shfl_up(g, d, 64);
     if (lane >= d) {
       v += ov;
       f += of;
+      g += og;
     }
   }
-  __shared__ int s_wv[16], s_wf[16];
+  __shared__ int s_wv[16], s_wf[16], s_wg[16];
   if (lane == 63) {
     s_wv[wave] = v;
     s_wf[wave] = f;
+    s_wg[wave] = g;
   }
   __syncthreads();
-  int pv = 0, pf = 0;
+  int pv = 0, pf = 0, pg = 0;
   for (int w = 0; w < wave; ++w) {
     pv += s_wv[w];
     pf += s_wf[w];
+    pg += s_wg[w];
   }
   const int base_e = pv + v - tot;           // exclusive
   const int run_i = pf + f - (tot > 0 ? 1 : 0);
+  const int pass_i = pg + g - npass;
   if (t < E) {
     int run = base_e;
     for (int w = 0; w < 16; ++w) {
@@ -300,11 +307,20 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       a.run_off[run_i] = base_e;
       a.run_len[run_i] = tot;
     }
+    for (int j = 0; j < npass; ++j) {
+      a.pass_expert[pass_i + j] = t;
+      a.pass_off[pass_i + j] = base_e + j * kLongRows;
+      a.pass_len[pass_i + j] = min(kLongRows, tot - j * kLongRows);
+    }
   }
   if (t == 1023) {
-    int nrun = 0;
-    for (int w = 0; w < 16; ++w) nrun += s_wf[w];
+    int nrun = 0, npas = 0;
+    for (int w = 0; w < 16; ++w) {
+      nrun += s_wf[w];
+      npas += s_wg[w];
+    }
     *a.n_runs = nrun;
+    *a.n_passes = npas;
   }
   __syncthreads();
   for (int c = pbeg; c < pend; c += 64) {
@@ -357,7 +373,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   if (gw >= (int64_t)a.N * n_cb) return;
   const int row = (int)(gw / n_cb), cb = (int)(gw % n_cb);
   const int c = cb * 128 + 2 * lane;
-  const int n_sl = n_slices(a.I / 16);
+  const int n_sl = a.fold ? 1 : n_slices(a.I / 16);  // down partials per output
   const int64_t plane = a.H;  // floats between slice planes of one slot
   float r0 = 0.0f, r1 = 0.0f;
   for (int k0 = 0; k0 < a.topk; k0 += kCombineBatch) {
@@ -429,7 +445,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   if (a.shared_kind == exl3m::kSharedTrellis) {
     const int64_t slot = (int64_t)a.P + row;
     const float2 ys = exl3m::ordered_sum2<4>(a.yhat_dn + slot * a.S_dn * plane + c, plane,
-                                                          n_slices(a.SI / 16));
+                                             a.fold ? 1 : n_slices(a.SI / 16));
     float y0, y1;
     down_out(ys, *reinterpret_cast<const uint32_t *>(a.tab[a.E].svh[2] + c), y0, y1);
     r0 += y0;
@@ -493,9 +509,9 @@ namespace {
 struct MoeLayout {
   size_t total;
   size_t logits, weights, ids, sorted_row, sorted_rank, slot_e, slot, run_expert, run_off, run_len,
-      n_runs;
+      n_runs, pass_expert, pass_off, pass_len, n_passes;
   size_t yhat_gu, act, yhat_dn, dsh_gu, dsh_act, dsh_dn;
-  int P, R, Imax, S_dn;
+  int P, R, Imax, S_dn, max_passes;
 };
 
 MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
@@ -523,6 +539,11 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.run_off = take(4 * (size_t)m.R);
   m.run_len = take(4 * (size_t)m.R);
   m.n_runs = take(4);
+  m.max_passes = m.R + (m.P + kLongRows - 1) / kLongRows;
+  m.pass_expert = take(4 * (size_t)m.max_passes);
+  m.pass_off = take(4 * (size_t)m.max_passes);
+  m.pass_len = take(4 * (size_t)m.max_passes);
+  m.n_passes = take(4);
   m.yhat_gu = take(4 * (size_t)slots * 2 * moe_slices(H) * m.Imax);
   m.act = take(2 * (size_t)slots * m.Imax);
   m.S_dn = std::max(moe_slices(I), SI > 0 ? moe_slices(SI) : 1);
@@ -553,7 +574,8 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.swiglu_limit = L->cfg.swiglu_limit;
   a.shared_kind = L->shared;
   a.logit_splits = dense_mfma_splits(a.H);
-  a.n_logit_blocks = (dense_mfma_tasks(a.H, a.E) + 3) / 4;
+  a.n_logit_blocks = (int)((dense_mfma_tasks(N, a.H, a.E) + 3) / 4);
+  a.fold = N > 16;  // long runs: kLongRows-row passes, slices folded in the workgroup
   a.pass_rows = (int)std::min<int64_t>(N, 16);
   a.h = h;
   a.router_w = L->router_w;
@@ -571,6 +593,10 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.run_off = (int32_t *)(ws + m.run_off);
   a.run_len = (int32_t *)(ws + m.run_len);
   a.n_runs = (int32_t *)(ws + m.n_runs);
+  a.pass_expert = (int32_t *)(ws + m.pass_expert);
+  a.pass_off = (int32_t *)(ws + m.pass_off);
+  a.pass_len = (int32_t *)(ws + m.pass_len);
+  a.n_passes = (int32_t *)(ws + m.n_passes);
   a.yhat_gu = (float *)(ws + m.yhat_gu);
   a.act = (uint16_t *)(ws + m.act);
   a.yhat_dn = (float *)(ws + m.yhat_dn);
@@ -861,32 +887,28 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[1], st));
 
-  const int H = layer->H, I = layer->I, SI = layer->SI;
+  const int H = layer->H;
   // L3: routed gate/up (+ the f16 shared expert's gate/up partials)
   const bool dense_sh = layer->shared == exl3m::kSharedDense;
-  const int gu_sl = moe_slices(H);
-  rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, (unsigned)((int64_t)m.R * 2 * (I / 128) * gu_sl),
-                         a, 0, dense_sh ? shared_gate_up_blocks(H, SI) : 0, st);
+  const int64_t units = a.fold ? m.max_passes : m.R;  // work units: runs or long-run passes
+  rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, units, a, 0, dense_sh, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[2], st));
   // L4: routed SwiGLU activations (+ the f16 shared expert's SwiGLU), L5: routed down
   // (+ the f16 shared expert's down partials)
-  rc = launch_moe_act(a, 0, dense_sh ? shared_swiglu_blocks(N, SI) : 0, st);
+  rc = launch_moe_act(a, 0, dense_sh ? shared_swiglu_blocks(N, layer->SI) : 0, st);
   if (rc) return rc;
-  rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb,
-                         (unsigned)((int64_t)m.R * (H / 128) * moe_slices(I)), a, 0,
-                         dense_sh ? shared_down_blocks(H, SI) : 0, st);
+  rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb, units, a, 0, dense_sh, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[3], st));
   // a trellis shared expert: one run of every token row through the same kernels
   if (layer->shared == exl3m::kSharedTrellis) {
-    rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, (unsigned)(2 * (SI / 128) * gu_sl), a, 1,
-                           0, st);
+    const int64_t sh_units = a.fold ? (N + kLongRows - 1) / kLongRows : 1;
+    rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, sh_units, a, 1, false, st);
     if (rc) return rc;
     rc = launch_moe_act(a, 1, 0, st);
     if (rc) return rc;
-    rc = launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, (unsigned)((H / 128) * moe_slices(SI)),
-                           a, 1, 0, st);
+    rc = launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, sh_units, a, 1, false, st);
     if (rc) return rc;
   }
   // L6: combine

@@ -35,6 +35,11 @@ struct ExpertTab {
 enum SharedKind { kSharedNone = 0, kSharedTrellis = 1, kSharedDense = 2 };
 
 // Everything a kernel of one layer call needs, passed by value.
+// Long-run mode (calls of more than 16 token rows): the expert kernels take passes of
+// up to kLongBlocks 16-row MFMA blocks per decode.
+constexpr int kLongBlocks = 3;
+constexpr int kLongRows = 16 * kLongBlocks;
+
 struct MoeArgs {
   // shape / config
   int N;       // token rows (B * L)
@@ -48,6 +53,7 @@ struct MoeArgs {
   int shared_kind;    // SharedKind
   int n_logit_blocks; // L1 workgroups computing router logits
   int logit_splits;   // k-split partials per logit (0: plain logits given by the caller)
+  int fold;           // 1: expert kernels fold their k slices (one partial per output)
   int pass_rows;      // token rows per MFMA pass of the expert kernels (<= 16)
   // inputs
   const uint16_t *h;          // (N, H) f16
@@ -64,7 +70,11 @@ struct MoeArgs {
   int32_t *slot_e;       // (P): slot -> expert
   int32_t *slot;         // (P): pair b*topk + k -> slot
   int32_t *run_expert, *run_off, *run_len;  // (R)
-  int32_t *n_runs;       // (1)
+  int32_t *n_runs;
+  int32_t *pass_expert;  // (R + ceil(P / kLongRows)) runs cut into passes of <= kLongRows rows
+  int32_t *pass_off;
+  int32_t *pass_len;
+  int32_t *n_passes;       // (1)
   float *yhat_gu;      // (P + N, 2, S, Imax): gate/up k-slice partials (S slices of H)
                        // before the output Hadamard
   uint16_t *act;       // (P + N, Imax): rotated SwiGLU output per slot, MFMA k order

@@ -25,11 +25,12 @@ __device__ __forceinline__ float swiglu1(float g, float u, float L) {
 // (out, in), both f16 row-major (the router weight as stored; the f16 shared expert's
 // weights transposed once when the layer is created). Products of f16 values are exact
 // in f32, so only the summation order differs from a scalar f32 dot product. `in` is
-// cut into S = dense_mfma_splits(in) <= 8 equal k splits; a wave task is (16 outputs,
-// one split): lane l loads 8 consecutive k of output 16nb + l%16 (the B operand,
-// k-group l/16) and of token row r0 + l%16 (the A operand), CHUNK 32-k steps at a time,
-// and accumulates the 16x16x32 MFMAs in step order. Split partials are written to
-// part[(row * out + n) * kDenseSlots + split] and summed in split order by the consumer.
+// cut into S = dense_mfma_splits(in) <= 8 equal k splits; a wave task is (16 token
+// rows, 16 outputs, one split): lane l loads 8 consecutive k of output 16nb + l%16 (the
+// B operand, k-group l/16) and of token row 16rb + l%16 (the A operand), CHUNK 32-k
+// steps at a time, and accumulates the 16x16x32 MFMAs in step order. Split partials
+// are written to part[(row * out + n) * kDenseSlots + split] and summed in split order
+// by the consumer.
 typedef _Float16 f16x8_ __attribute__((ext_vector_type(8)));
 typedef float f32x4_ __attribute__((ext_vector_type(4)));
 
@@ -39,42 +40,44 @@ constexpr int kLogitChunk = 16;  // MFMA steps per load round of the router logi
 __host__ __device__ constexpr int dense_mfma_splits(int in) {
   return (in / 128) % 8 == 0 ? 8 : ((in / 128) % 4 == 0 ? 4 : ((in / 128) % 2 == 0 ? 2 : 1));
 }
-__host__ __device__ inline int dense_mfma_tasks(int in, int out) {
-  return ((out + 15) / 16) * dense_mfma_splits(in);
+// Wave tasks of an (rows x in) @ (in x out) dense GEMV.
+__host__ __device__ inline int64_t dense_mfma_tasks(int64_t rows, int in, int out) {
+  return ((rows + 15) / 16) * ((out + 15) / 16) * dense_mfma_splits(in);
 }
 
 template <int CHUNK>
 __device__ __forceinline__ void dense_mfma(const uint16_t *__restrict__ x, int64_t rows, int in,
                                            const uint16_t *__restrict__ wt, int out,
-                                           float *__restrict__ part, int task) {
+                                           float *__restrict__ part, int64_t task) {
   const int lane = threadIdx.x & 63;
   const int S = dense_mfma_splits(in), sk = in / S, nsteps = sk / 32;
-  const int nb = task / S, sp = task % S;
+  const int n_nb = (out + 15) / 16;
+  const int sp = (int)(task % S);
+  const int nb = (int)((task / S) % n_nb);
+  const int64_t r0 = 16 * (task / ((int64_t)S * n_nb));
   const int n = nb * 16 + (lane & 15), g = lane >> 4;
   const int nc = n < out ? n : out - 1;  // out-of-range outputs load a valid row, never stored
   const int k0 = sp * sk + 8 * g;
-  for (int64_t r0 = 0; r0 < rows; r0 += 16) {
-    const int64_t row = r0 + (lane & 15);
-    const int64_t rc = row < rows ? row : rows - 1;
-    f32x4_ D = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t row = r0 + (lane & 15);
+  const int64_t rc = row < rows ? row : rows - 1;
+  f32x4_ D = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 1
-    for (int q0 = 0; q0 < nsteps; q0 += CHUNK) {
-      f16x8_ A[CHUNK], B[CHUNK];
+  for (int q0 = 0; q0 < nsteps; q0 += CHUNK) {
+    f16x8_ A[CHUNK], B[CHUNK];
 #pragma unroll
-      for (int q = 0; q < CHUNK; ++q) {
-        const int k = k0 + 32 * min(q0 + q, nsteps - 1);
-        B[q] = *reinterpret_cast<const f16x8_ *>(wt + (int64_t)nc * in + k);
-        A[q] = *reinterpret_cast<const f16x8_ *>(x + rc * in + k);
-      }
-#pragma unroll
-      for (int q = 0; q < CHUNK; ++q)
-        if (q0 + q < nsteps) D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[q], B[q], D, 0, 0, 0);
+    for (int q = 0; q < CHUNK; ++q) {
+      const int k = k0 + 32 * min(q0 + q, nsteps - 1);
+      B[q] = *reinterpret_cast<const f16x8_ *>(wt + (int64_t)nc * in + k);
+      A[q] = *reinterpret_cast<const f16x8_ *>(x + rc * in + k);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t rr = r0 + 4 * g + i;
-      if (rr < rows && n < out) part[(rr * out + n) * kDenseSlots + sp] = D[i];
-    }
+    for (int q = 0; q < CHUNK; ++q)
+      if (q0 + q < nsteps) D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[q], B[q], D, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t rr = r0 + 4 * g + i;
+    if (rr < rows && n < out) part[(rr * out + n) * kDenseSlots + sp] = D[i];
   }
 }
 
@@ -91,17 +94,18 @@ __device__ __forceinline__ float dense_slots_sum(const float *p, int S) {
 }
 
 // The f16 shared expert (g5_linear's mx::matmul branch, glm5_kda.cpp:120; SwiGLU as in
-// glm5_moe.cpp:66-74) as extra workgroups (4 waves, one MFMA task per wave) of the
+// glm5_moe.cpp:66-74) as extra workgroups (one MFMA task per wave) of the
 // routed expert launches: the gate/up partials beside the routed gate/up, their SwiGLU
 // beside the routed activations, the down partials beside the routed down (the combine
 // sums those in split order). Weights: the layer's transposed (out, in) copies.
 constexpr int kSharedChunk = 4;  // MFMA steps per load round (keeps the expert kernels' VGPRs)
 
-__host__ __device__ inline int shared_gate_up_blocks(int H, int SI) {
-  return (2 * dense_mfma_tasks(H, SI) + 3) / 4;
+// Workgroups of `waves` waves, one task per wave.
+__host__ __device__ inline int shared_gate_up_blocks(int64_t N, int H, int SI, int waves) {
+  return (int)((2 * dense_mfma_tasks(N, H, SI) + waves - 1) / waves);
 }
-__host__ __device__ inline int shared_down_blocks(int H, int SI) {
-  return (dense_mfma_tasks(SI, H) + 3) / 4;
+__host__ __device__ inline int shared_down_blocks(int64_t N, int H, int SI, int waves) {
+  return (int)((dense_mfma_tasks(N, SI, H) + waves - 1) / waves);
 }
 __host__ __device__ inline int shared_swiglu_blocks(int64_t N, int SI) {
   return (int)((N * SI / 2 + 255) / 256);
@@ -109,13 +113,13 @@ __host__ __device__ inline int shared_swiglu_blocks(int64_t N, int SI) {
 
 __device__ __forceinline__ void shared_gate_up_block(const uint16_t *h, int64_t N, int H, int SI,
                                                      const uint16_t *wg_t, const uint16_t *wu_t,
-                                                     float *dsh_gu, int b) {
-  const int per = dense_mfma_tasks(H, SI);
-  const int task = b * 4 + (threadIdx.x >> 6);
+                                                     float *dsh_gu, int b, int waves) {
+  const int64_t per = dense_mfma_tasks(N, H, SI);
+  const int64_t task = (int64_t)b * waves + (threadIdx.x >> 6);
   if (task >= 2 * per) return;
-  const int proj = task / per;
+  const int proj = task >= per;
   dense_mfma<kSharedChunk>(h, N, H, proj ? wu_t : wg_t, SI,
-                           dsh_gu + (int64_t)proj * N * SI * kDenseSlots, task % per);
+                           dsh_gu + (int64_t)proj * N * SI * kDenseSlots, task - proj * per);
 }
 
 // One element pair (i, i + 1) per thread of 256-thread workgroup b.
@@ -135,9 +139,10 @@ __device__ __forceinline__ void shared_swiglu_block(const float *dsh_gu, int64_t
 }
 
 __device__ __forceinline__ void shared_down_block(const uint16_t *dsh_act, int64_t N, int H, int SI,
-                                                  const uint16_t *wd_t, float *dsh_dn, int b) {
-  const int task = b * 4 + (threadIdx.x >> 6);
-  if (task >= dense_mfma_tasks(SI, H)) return;
+                                                  const uint16_t *wd_t, float *dsh_dn, int b,
+                                                  int waves) {
+  const int64_t task = (int64_t)b * waves + (threadIdx.x >> 6);
+  if (task >= dense_mfma_tasks(N, SI, H)) return;
   dense_mfma<kSharedChunk>(dsh_act, N, SI, wd_t, H, dsh_dn, task);
 }
 

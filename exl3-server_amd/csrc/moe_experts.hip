@@ -76,7 +76,8 @@ template <int K, int CB, int PD>
 __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
   if ((int)blockIdx.x < dense_blocks) {
-    shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu, blockIdx.x);
+    shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu, blockIdx.x,
+                         kGuThreads / 64);
     return;
   }
   const int out = shared_mode ? a.SI : a.I;
@@ -140,7 +141,7 @@ template <int K, int CB, int PD>
 __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
   if ((int)blockIdx.x < dense_blocks) {
-    shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn, blockIdx.x);
+    shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn, blockIdx.x, kDnThreads / 64);
     return;
   }
   const int in = shared_mode ? a.SI : a.I;
@@ -185,6 +186,174 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8
   }
 }
 
+// Long runs (calls of more than 16 token rows): 8-wave workgroups, wave w owns n-pair
+// 8*cb + w, passes of up to kLongRows rows with kLongBlocks 16-row MFMA blocks per
+// decode (qmv_slice_rb), and every k slice of the tensor in one workgroup: the slice
+// partials are added in slice order in registers (acc = p0; acc += p1; ...), the
+// same f32 operations as the slice-order sum of the short-run path, so each output
+// bit matches it. One partial per output goes to slice position 0.
+using exl3m::kLongBlocks;
+using exl3m::kLongRows;
+constexpr int kLongThreads = 512;
+
+// Work unit u of the long-run kernels: pass u of the dispatch's pass table, or (shared
+// mode) rows [u * kLongRows, u * kLongRows + kLongRows) of the trellis shared expert.
+__device__ __forceinline__ bool pass_info(const MoeArgs &a, int u, int shared_mode, RunInfo &ri) {
+  if (shared_mode) {
+    if (u * kLongRows >= a.N) return false;
+    ri.e = a.E;
+    ri.off = a.P + u * kLongRows;
+    ri.len = min(kLongRows, a.N - u * kLongRows);
+    return true;
+  }
+  if (u >= *a.n_passes) return false;
+  ri.e = a.pass_expert[u];
+  ri.off = a.pass_off[u];
+  ri.len = a.pass_len[u];
+  return true;
+}
+
+template <int RB>
+__device__ __forceinline__ void fold_partials(f32x4 (&acc)[RB][2], const f32x4 (&D)[RB][2], bool first) {
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[r][h][i] = first ? D[r][h][i] : acc[r][h][i] + D[r][h][i];
+}
+
+template <int K, int CB, int PD>
+__global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_moe_gate_up_long(MoeArgs a, int shared_mode, int dense_blocks) {
+  extern __shared__ uint32_t smem[];
+  constexpr int kWaves = kLongThreads / 64;
+  if ((int)blockIdx.x < dense_blocks) {
+    shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu, blockIdx.x,
+                         kWaves);
+    return;
+  }
+  const int out = shared_mode ? a.SI : a.I;
+  const int n_np = out / 32, n_cb = (n_np + kWaves - 1) / kWaves;
+  const int k_tiles = a.H / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
+  int b = blockIdx.x - dense_blocks;
+  const int cb = b % n_cb;
+  b /= n_cb;
+  const int proj = b & 1, u = b >> 1;
+  RunInfo ri;
+  if (!pass_info(a, u, shared_mode, ri)) return;
+  const exl3m::ExpertTab &tb = a.tab[ri.e];
+  const uint32_t *base = tb.tr[proj];
+  const uint16_t *suh = tb.suh[proj];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int np = cb * kWaves + wave;
+  const bool active = np < n_np;  // idle waves still stage rows and meet the barriers
+  const int slice_k = kStepTiles * ss * 16;
+  const int nblk = slice_k / 128;
+  const int xs_stride = slice_k / 2;
+  uint32_t *xs = smem;
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * kSlotChunks;
+
+  for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
+    const int nr = min(kLongRows, ri.len - p0);
+    f32x4 acc[kLongBlocks][2];
+    for (int sl = 0; sl < n_sl; ++sl) {
+      const int k_base = sl * slice_k;
+      for (int bi = wave; bi < nr * nblk; bi += kWaves) {
+        const int r = bi / nblk, blk = bi % nblk;
+        const int row = a.sorted_row[ri.off + p0 + r];
+        const int kc = k_base + blk * 128 + 2 * lane;
+        const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
+        const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
+        float v0 = lo16(hx), v1 = hi16(hx);
+        wave_had_pre(v0, v1, lo16(sx), hi16(sx));
+        stage_pair(xs + r * xs_stride, blk, lane, pack16(v0, v1));
+      }
+      __syncthreads();
+      if (active) {
+        f32x4 D[kLongBlocks][2];
+        qmv_slice_rb<K, CB, PD, kLongBlocks>(base, k_tiles, out / 16, sl * kStepTiles * ss, np, ss,
+                                             xs, xs_stride, nr, slot, D);
+        fold_partials<kLongBlocks>(acc, D, sl == 0);
+      }
+      __syncthreads();
+    }
+    if (active) {
+      const int col = np * 32;
+#pragma unroll
+      for (int rb = 0; rb < kLongBlocks; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * rb + d_row(i);
+          if (r < nr) {
+            float *y = a.yhat_gu + (int64_t)((ri.off + p0 + r) * 2 + proj) * n_sl * a.Imax + col;
+            y[d_col(0)] = acc[rb][0][i];
+            y[d_col(1)] = acc[rb][1][i];
+          }
+        }
+    }
+  }
+}
+
+template <int K, int CB, int PD>
+__global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_moe_down_long(MoeArgs a, int shared_mode, int dense_blocks) {
+  extern __shared__ uint32_t smem[];
+  constexpr int kWaves = kLongThreads / 64;
+  if ((int)blockIdx.x < dense_blocks) {
+    shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn, blockIdx.x, kWaves);
+    return;
+  }
+  const int in = shared_mode ? a.SI : a.I;
+  const int n_np = a.H / 32, n_cb = (n_np + kWaves - 1) / kWaves;
+  const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
+  const int b = blockIdx.x - dense_blocks;
+  const int cb = b % n_cb, u = b / n_cb;
+  RunInfo ri;
+  if (!pass_info(a, u, shared_mode, ri)) return;
+  const exl3m::ExpertTab &tb = a.tab[ri.e];
+  const int wave = threadIdx.x >> 6;
+  const int np = cb * kWaves + wave;
+  const bool active = np < n_np;
+  const int slice_k = kStepTiles * ss * 16;
+  const int xs_stride = slice_k / 2;
+  const int q_row = xs_stride / 4;  // 16-byte chunks per staged row
+  uint32_t *xs = smem;
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * kSlotChunks;
+
+  for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
+    const int nr = min(kLongRows, ri.len - p0);
+    f32x4 acc[kLongBlocks][2];
+    for (int sl = 0; sl < n_sl; ++sl) {
+      for (int i = threadIdx.x; i < nr * q_row; i += kLongThreads) {
+        const int r = i / q_row, q = i % q_row;
+        reinterpret_cast<uint4 *>(xs + r * xs_stride)[q] = reinterpret_cast<const uint4 *>(
+            a.act + (int64_t)(ri.off + p0 + r) * a.Imax + sl * slice_k)[q];
+      }
+      __syncthreads();
+      if (active) {
+        f32x4 D[kLongBlocks][2];
+        qmv_slice_rb<K, CB, PD, kLongBlocks>(tb.tr[2], k_tiles, a.H / 16, sl * kStepTiles * ss, np,
+                                             ss, xs, xs_stride, nr, slot, D);
+        fold_partials<kLongBlocks>(acc, D, sl == 0);
+      }
+      __syncthreads();
+    }
+    if (active) {
+      const int col = np * 32;
+#pragma unroll
+      for (int rb = 0; rb < kLongBlocks; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * rb + d_row(i);
+          if (r < nr) {
+            float *y = a.yhat_dn + (int64_t)(ri.off + p0 + r) * a.S_dn * a.H + col;
+            y[d_col(0)] = acc[rb][0][i];
+            y[d_col(1)] = acc[rb][1][i];
+          }
+        }
+    }
+  }
+}
+
 // One wave per (slot, 128-block of the intermediate): the gate/up slice partials
 // summed in slice order, their output Hadamards (svh), SwiGLU with the swiglu_limit
 // clamp (f16 op by op), and the down projection's input Hadamard (suh) -> act (f16, in
@@ -205,13 +374,14 @@ __global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_m
   if (gw >= (int64_t)n_slots * nblk) return;
   const int blk = (int)(gw % nblk);
   const int64_t slot = (shared_mode ? a.P : 0) + gw / nblk;
-  const int gu_sl = n_slices(a.H / 16);
+  const int gu_stride = n_slices(a.H / 16);       // slice positions per (slot, projection)
+  const int gu_sl = a.fold ? 1 : gu_stride;        // partials to sum
   const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
   const int c = blk * 128 + 2 * lane;
   // the slice partials are loaded while the expert's scale pointers are fetched
   constexpr int kMaxSl = 8;
-  const float *pg = a.yhat_gu + (slot * 2 + 0) * gu_sl * a.Imax + c;
-  const float *pu = a.yhat_gu + (slot * 2 + 1) * gu_sl * a.Imax + c;
+  const float *pg = a.yhat_gu + (slot * 2 + 0) * gu_stride * a.Imax + c;
+  const float *pu = a.yhat_gu + (slot * 2 + 1) * gu_stride * a.Imax + c;
   float2 vg[kMaxSl], vu[kMaxSl];
 #pragma unroll
   for (int q = 0; q < kMaxSl; ++q) {
@@ -264,29 +434,39 @@ size_t moe_down_lds(int in, int pass_rows) { return expert_lds(in, pass_rows, kD
 int moe_slices(int in) { return n_slices(in / 16); }
 
 
+template <typename Kern>
+static exl3_status launch_kernel(Kern k, unsigned blocks, unsigned threads, size_t lds, hipStream_t st,
+                                 const MoeArgs &a, int shared_mode, int dense_blocks, bool &attr_set) {
+  if (!attr_set) {
+    EXL3_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 160 * 1024));
+    attr_set = true;
+  }
+  k<<<blocks, threads, lds, st>>>(a, shared_mode, dense_blocks);
+  return EXL3_OK;
+}
+
+// which: 0 = gate/up, 1 = down.
 template <int K, int CB, int PD>
 static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
                           int shared_mode, int dense_blocks) {
-  if (which == 0) {
-    const size_t lds = moe_gate_up_lds(a.H, a.pass_rows);
-    static bool attr_set = false;
-    if (!attr_set) {
-      EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_gate_up<K, CB, PD>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-      attr_set = true;
-    }
-    k_moe_gate_up<K, CB, PD><<<blocks, kGuThreads, lds, st>>>(a, shared_mode, dense_blocks);
-  } else {
-    const size_t lds = moe_down_lds(shared_mode ? a.SI : a.I, a.pass_rows);
-    static bool attr_set = false;
-    if (!attr_set) {
-      EXL3_HIP(hipFuncSetAttribute((const void *)k_moe_down<K, CB, PD>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-      attr_set = true;
-    }
-    k_moe_down<K, CB, PD><<<blocks, kDnThreads, lds, st>>>(a, shared_mode, dense_blocks);
+  const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
+  if (a.fold) {
+    const size_t lds = expert_lds(in, kLongRows, kLongThreads / 64);
+    static bool set_gu = false, set_dn = false;
+    return which == 0 ? launch_kernel(k_moe_gate_up_long<K, CB, PD>, blocks, kLongThreads, lds, st, a,
+                                      shared_mode, dense_blocks, set_gu)
+                      : launch_kernel(k_moe_down_long<K, CB, PD>, blocks, kLongThreads, lds, st, a,
+                                      shared_mode, dense_blocks, set_dn);
   }
-  return EXL3_OK;
+  static bool set_gu = false, set_dn = false;
+  return which == 0
+             ? launch_kernel(k_moe_gate_up<K, CB, PD>, blocks, kGuThreads,
+                             expert_lds(in, a.pass_rows, kGuThreads / 64), st, a, shared_mode,
+                             dense_blocks, set_gu)
+             : launch_kernel(k_moe_down<K, CB, PD>, blocks, kDnThreads,
+                             expert_lds(in, a.pass_rows, kDnThreads / 64), st, a, shared_mode,
+                             dense_blocks, set_dn);
 }
 
 template <int K, int CB>
@@ -312,20 +492,35 @@ static int moe_prefetch(int k_tiles, int K) {
   return pd;
 }
 
-// which: 0 = gate/up, 1 = down; `blocks` routed workgroups after `dense_blocks` f16
-// shared-expert workgroups.
-exl3_status launch_moe_expert(int which, int K, int cb, unsigned blocks, const MoeArgs &a,
-                              int shared_mode, int dense_blocks, hipStream_t st) {
-  blocks += (unsigned)dense_blocks;
-  if (blocks == 0) return EXL3_OK;
+// which: 0 = gate/up, 1 = down, over `runs` runs (routed: the dispatch's run table,
+// bounded by R; shared_mode 1: the one trellis-shared run). dense: prepend the f16
+// shared expert's workgroups for this projection.
+exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeArgs &a,
+                              int shared_mode, bool dense, hipStream_t st) {
   const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
+  const int out = which == 0 ? (shared_mode ? a.SI : a.I) : a.H;
+  const int n_sl = n_slices(in / 16);
+  const int waves = a.fold ? kLongThreads / 64 : kGuThreads / 64;
+  int64_t blocks;
+  if (a.fold)
+    blocks = runs * (which == 0 ? 2 : 1) * ((out / 32 + waves - 1) / waves);
+  else
+    blocks = runs * (which == 0 ? 2 : 1) * (out / 128) * n_sl;
+  const int dense_blocks =
+      !dense ? 0
+             : (which == 0 ? shared_gate_up_blocks(a.N, a.H, a.SI, waves)
+                           : shared_down_blocks(a.N, a.H, a.SI, waves));
+  blocks += dense_blocks;
+  if (blocks == 0) return EXL3_OK;
+  if (blocks > 0x7fffffff) return fail(EXL3_ERR_UNSUPPORTED, "expert launch too large");
   const int pd = moe_prefetch(in / 16, K);
   exl3_status rc = EXL3_OK;
-#define EXL3_KC(KK)                                                                               \
-  case KK:                                                                                        \
-    if (cb == 0) rc = moe_pd<KK, 0>(pd, which, blocks, st, a, shared_mode, dense_blocks);        \
-    else if (cb == 1) rc = moe_pd<KK, 1>(pd, which, blocks, st, a, shared_mode, dense_blocks);   \
-    else rc = moe_pd<KK, 2>(pd, which, blocks, st, a, shared_mode, dense_blocks);                \
+  const unsigned ub = (unsigned)blocks;
+#define EXL3_KC(KK)                                                                            \
+  case KK:                                                                                     \
+    if (cb == 0) rc = moe_pd<KK, 0>(pd, which, ub, st, a, shared_mode, dense_blocks);         \
+    else if (cb == 1) rc = moe_pd<KK, 1>(pd, which, ub, st, a, shared_mode, dense_blocks);    \
+    else rc = moe_pd<KK, 2>(pd, which, ub, st, a, shared_mode, dense_blocks);                 \
     break;
   switch (K) {
     EXL3_KC(1) EXL3_KC(2) EXL3_KC(3) EXL3_KC(4) EXL3_KC(5) EXL3_KC(6) EXL3_KC(7) EXL3_KC(8)

@@ -245,6 +245,86 @@ __device__ __forceinline__ void qmv_slice(const uint32_t *base, int k_tiles, int
   }
 }
 
+// Long runs: RB blocks of 16 token rows share one decode. The four B operands of a
+// wave step are decoded once and each block b runs its 4 MFMAs with its own A
+// operands (staged row 16b + l%16 at word offset xo[b] of xs) and accumulators; per
+// block the accumulation is exactly mfma_step's, so every row's result is
+// bit-identical to a 16-row pass.
+template <int K, int CB, int RB>
+__device__ __forceinline__ void mfma_step_rb(const uint32_t (&W)[K + 1], const uint32_t *xs,
+                                             const int (&xo)[RB], f32x4 (&D)[RB][2]) {
+  uint32_t F[K + 1];
+  lane_funnels<K>(W, F);
+  // k-rows 0..7 of the step (A0) before 8..15 (A1), as in mfma_step; two B operands
+  // live at a time
+  const f16x8 B0 = b_operand<K, CB, 0>(W, F), B1 = b_operand<K, CB, 4>(W, F);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const f16x8 A0 = *reinterpret_cast<const f16x8 *>(xs + xo[r]);
+    D[r][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B0, D[r][0], 0, 0, 0);
+    D[r][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B1, D[r][1], 0, 0, 0);
+  }
+  const f16x8 B2 = b_operand<K, CB, 16>(W, F), B3 = b_operand<K, CB, 20>(W, F);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const f16x8 A1 = *reinterpret_cast<const f16x8 *>(xs + xo[r] + 4);
+    D[r][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B2, D[r][0], 0, 0, 0);
+    D[r][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B3, D[r][1], 0, 0, 0);
+  }
+}
+
+// qmv_slice over up to 16 * RB staged token rows: xs = the first staged row (row
+// stride xs_stride words), nrows = rows staged (>= 1); rows past nrows read the last
+// row and are never stored. D[b] = the slice partials of rows 16b .. 16b + 15.
+template <int K, int CB, int PD, int RB>
+__device__ __forceinline__ void qmv_slice_rb(const uint32_t *base, int k_tiles, int tiles_n, int kt0,
+                                             int np, int nsteps, const uint32_t *xs, int xs_stride,
+                                             int nrows, u32x4 *slot, f32x4 (&D)[RB][2]) {
+  static_assert(16 * K <= kSlotChunks, "slot size");
+  const StepLane sl = step_lane();
+  const int lane = threadIdx.x & 63;
+  constexpr uint32_t kTileBytes = 32 * K;
+  constexpr int kChunks = 16 * K, kRowChunks = 4 * K;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)base, (short)0, (int)((uint32_t)k_tiles * tiles_n * kTileBytes), 0x00020000);
+  const uint32_t step_bytes = (uint32_t)kStepTiles * tiles_n * kTileBytes;
+  auto chunk_off = [&](int c) -> uint32_t {
+    return c < kChunks ? ((uint32_t)(c / kRowChunks) * tiles_n + 2 * np) * kTileBytes +
+                             (uint32_t)(c % kRowChunks) * 16
+                       : kNoChunk;
+  };
+  const uint32_t vo0 = chunk_off(lane), vo1 = chunk_off(64 + lane);
+  const int wbase = (sl.kt * 2 + sl.nt) * 8 * K;
+  const uint32_t so0 = (uint32_t)kt0 * tiles_n * kTileBytes;
+  int xo[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) xo[r] = min(16 * r + (lane & 15), nrows - 1) * xs_stride + sl.kt * 8;
+  StepLoads<K> L[PD];
+#pragma unroll
+  for (int b = 0; b < PD; ++b) step_load<K>(rsrc, vo0, vo1, so0 + b * step_bytes, L[b]);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    D[r][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    D[r][1] = D[r][0];
+  }
+  int s0 = 0;
+  for (; s0 < nsteps - PD; s0 += PD) {
+#pragma unroll
+    for (int b = 0; b < PD; ++b) {
+      uint32_t W[K + 1];
+      step_words<K>(slot, wbase, sl.m, L[b], W);
+      step_load<K>(rsrc, vo0, vo1, so0 + (s0 + b + PD) * step_bytes, L[b]);
+      mfma_step_rb<K, CB, RB>(W, xs + (s0 + b) * (kStepTiles * 8), xo, D);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < PD; ++b) {
+    uint32_t W[K + 1];
+    step_words<K>(slot, wbase, sl.m, L[b], W);
+    mfma_step_rb<K, CB, RB>(W, xs + (s0 + b) * (kStepTiles * 8), xo, D);
+  }
+}
+
 // Output position of accumulator element D_h[i] of this lane inside its n-pair's 32
 // columns: token row 4*(l/16) + i, column 16*nt + m + 8h.
 __device__ __forceinline__ int d_row(int i) { return 4 * ((threadIdx.x & 63) >> 4) + i; }

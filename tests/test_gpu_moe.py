@@ -141,7 +141,7 @@ def test_rows_path_equals_single_rows(dev):
                           shared_K=3, shared_cb=2)
     layer = synth.make_layer(cfg, 5)
     d = DeviceMoeLayer(layer, dev)
-    for B in (4, 11):
+    for B in (4, 11, 40, 100):  # 40, 100: the long-run path (runs of ~30 and ~75 rows)
         h = synth.activations(5, f"rows.{B}", B, 128)
         x = to_dev(h, dev, B, 1, 128)
         yb = d(x).cpu()
@@ -164,12 +164,16 @@ def test_repeat_calls_are_deterministic(dev):
     d.close()
 
 
-def glm5_layer_on_device(dev, seed, tag):
+def glm5_layer_on_device(dev, seed, tag, cfg=None, hot_experts=None, hot_bias=0.0):
     """Full-size GLM-5 layer: small tensors from numpy, trellis words on the device."""
-    cfg = synth.config_glm5()
+    cfg = cfg or synth.config_glm5()
     H, I, E = cfg.hidden, cfg.inter, cfg.n_experts
+    bias = synth.normal_f32(seed, f"{tag}.gate.e_score_correction_bias", (E,), 0, 0.01)
+    if hot_experts is not None:
+        bias = bias.copy()
+        bias[np.asarray(hot_experts)] += np.float32(hot_bias)
     layer = synth.MoeLayer(cfg, [], None, synth.normal_f16(seed, f"{tag}.gate.weight", (E, H), 0, 0.02),
-                           synth.normal_f32(seed, f"{tag}.gate.e_score_correction_bias", (E,), 0, 0.01))
+                           bias)
     words = {}
     for e in range(E):
         for j, (nm, i_f, o_f, K) in enumerate((("gate_proj", H, I, cfg.gate_up_K),
@@ -181,10 +185,27 @@ def glm5_layer_on_device(dev, seed, tag):
                                cb=cfg.gate_up_cb if j < 2 else cfg.down_cb)
             layer.experts.append(lin)
             words[3 * e + j] = trellis_words_torch(seed, p + ".trellis", i_f, o_f, K, dev)
-    layer.shared = [synth.make_dense_linear(seed, f"{tag}.shared_experts.gate_proj", H, 1024),
-                    synth.make_dense_linear(seed, f"{tag}.shared_experts.up_proj", H, 1024),
-                    synth.make_dense_linear(seed, f"{tag}.shared_experts.down_proj", 1024, H)]
+    SI = cfg.shared_inter
+    dims = ((f"{tag}.shared_experts.gate_proj", H, SI), (f"{tag}.shared_experts.up_proj", H, SI),
+            (f"{tag}.shared_experts.down_proj", SI, H))
+    if cfg.shared_K == 0:
+        layer.shared = [synth.make_dense_linear(seed, p, i_f, o_f) for p, i_f, o_f in dims]
+    else:
+        layer.shared = []
+        for j, (p, i_f, o_f) in enumerate(dims):
+            layer.shared.append(synth.Linear(i_f, o_f, trellis=None,
+                                             suh=synth.normal_f16(seed, p + ".suh", (i_f,), 1, 0.05),
+                                             svh=synth.normal_f16(seed, p + ".svh", (o_f,), 1, 0.05),
+                                             K=cfg.shared_K, cb=cfg.shared_cb))
+            words[("shared", j)] = trellis_words_torch(seed, p + ".trellis", i_f, o_f, cfg.shared_K, dev)
     return layer, words
+
+
+def oracle_linear(lin, w):
+    if lin.trellis is not None or w is None:
+        return lin.oracle_dict()
+    return dict(trellis=w.cpu().numpy().view(np.uint16), suh=lin.suh, svh=lin.svh, K=lin.K,
+                cb=lin.cb, **{"in": lin.in_f, "out": lin.out_f})
 
 
 def oracle_experts(layer, words, used):
@@ -192,15 +213,12 @@ def oracle_experts(layer, words, used):
     dummy = dict(trellis=np.zeros(16, np.uint16), suh=np.zeros(1, np.uint16),
                  svh=np.zeros(1, np.uint16), K=1, cb=0, **{"in": 16, "out": 16})
     for i, lin in enumerate(layer.experts):
-        if i // 3 in used:
-            d = dict(lin.oracle_dict()) if lin.trellis is not None else None
-            if d is None:
-                d = dict(trellis=words[i].cpu().numpy().view(np.uint16), suh=lin.suh, svh=lin.svh,
-                         K=lin.K, cb=lin.cb, **{"in": lin.in_f, "out": lin.out_f})
-            out.append(d)
-        else:
-            out.append(dummy)
+        out.append(oracle_linear(lin, words.get(i)) if i // 3 in used else dummy)
     return out
+
+
+def oracle_shared(layer, words):
+    return [oracle_linear(l, words.get(("shared", j))) for j, l in enumerate(layer.shared)]
 
 
 def test_glm5_layer_b8_vs_oracle(oracle, dev):
@@ -218,7 +236,7 @@ def test_glm5_layer_b8_vs_oracle(oracle, dev):
     idx, w, flips = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
     used = set(idx.reshape(-1).tolist())
     want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used),
-                                   [l.oracle_dict() for l in layer.shared], h, idx, w)
+                                   oracle_shared(layer, words), h, idx, w)
     rel, cos = check_out(y, want)
     dg = d.diag()
     assert dg["calls"] == 1 and dg["pairs"] == 64 and dg["distinct_experts"] == len(used)
@@ -251,9 +269,47 @@ def test_glm5_b64_run_grouping(oracle, dev):
     assert sum(1 for r in runs["run_len"] if r >= 48) >= 8
     used = set(idx.reshape(-1).tolist())
     want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used),
-                                   [l.oracle_dict() for l in layer.shared], h, idx, w)
+                                   oracle_shared(layer, words), h, idx, w)
     check_out(y, want)
     # the 48 identical rows give identical outputs
     yc = y.view(64, -1).cpu()
     assert all(torch.equal(yc[i], yc[0]) for i in range(48))
+    d.close()
+
+
+def test_prefill_2048_config5(oracle, dev):
+    # 2048 token rows; gate/up K4 3inst, down K5 mul1, shared expert K6 mcg;
+    # 8 hot experts take about a quarter of the selections (bias tilt 0.23)
+    cfg = synth.config_prefill()
+    hot = list(range(0, cfg.n_experts, cfg.n_experts // 8))
+    layer, words = glm5_layer_on_device(dev, 51, "pf", cfg, hot, 0.23)
+    N, H = 2048, cfg.hidden
+    h = synth.activations(51, "pf.x", N, H)
+    x = to_dev(h, dev, N, 1, H)
+    d = DeviceMoeLayer(layer, dev, words=words)
+    d.diag_enable()
+    y = d(x).view(N, H)
+    _, ids = d.route(x)
+    oc = ocfg_of(oracle, cfg, True)
+    logits = oracle.router_logits(h, layer.router_w)
+    idx, w, flips = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+    hot_frac = np.isin(idx, hot).mean()
+    assert 0.2 < hot_frac < 0.3, hot_frac
+    runs = oracle.moe_runs(idx)
+    hist = {}
+    for r in runs["run_len"].tolist():
+        hist[min(r, 64)] = hist.get(min(r, 64), 0) + 1
+    assert d.diag()["run_hist"] == hist
+    # sampled rows: single-row calls (the decode path) give the same bits, and the
+    # oracle agrees within the tolerance
+    rows = sorted(set(list(range(0, N, 171)) + [N - 1]))
+    yc = y.cpu()
+    for r in rows:
+        assert torch.equal(d(x[r:r + 1].contiguous()).view(-1).cpu(), yc[r]), r
+    used = set(idx[rows].reshape(-1).tolist())
+    want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used), oracle_shared(layer, words),
+                                   h[rows], idx[rows], w[rows])
+    rel, cos = check_out(yc[rows], want)
+    print(f"\nprefill 2048: hot fraction {hot_frac:.3f}, runs {len(runs['run_len'])}, "
+          f"max run {max(runs['run_len'])}, sampled max|err|/rms {rel:.3g}, cos {cos:.7f}, flips {flips}")
     d.close()
