@@ -12,6 +12,11 @@ combine) on one batch of 8 token rows. Steps rotate over --layers distinct layer
 instances (default 8, ~15.7 GB of trellis) with their own inputs, so consecutive steps
 stream different experts and the 256 MB MALL cannot serve a repeated working set.
 
+--workload picks the run: glm5_moe_decode_b8 (the default and the metric's workload),
+glm5_moe_staged_b64 (configs[3]: 48 identical rows + 16 independent rows, B=64) or
+glm5_moe_prefill_2048 (configs[4]: 2048 rows, gate/up K4 3inst, down K5 mul1, K6 mcg
+shared expert, 8 hot experts taking about a quarter of the selections).
+
 Output: one JSON line. `value` = 8 rows / (wall time per step) with inputs resident in
 HBM. `roofline` = the routed gate|up kernel (the dominant kernel): algorithmic trellis
 bytes of the distinct experts it streams per launch / its average launch time (HIP
@@ -31,6 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "exl3-server_amd"))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix peak
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_glm5_b8_traffic.md")
 
 
@@ -46,20 +52,34 @@ def measured_traffic(kernel):
     return int(m.group(1)) if m else None
 
 
-def build_layers(n_layers, seed, device):
+WORKLOADS = {
+    # name: (synth config, token rows per step, description)
+    "glm5_moe_decode_b8": ("glm5", 8, "configs[2]: GLM-5-shaped layer, decode batch 8"),
+    "glm5_moe_staged_b64": ("glm5", 64, "configs[3]: 48 identical rows + 16 independent rows"),
+    "glm5_moe_prefill_2048": ("prefill", 2048, "configs[4]: 2048-token prefill, gate/up K4 3inst, "
+                                               "down K5 mul1, shared K6 mcg, 8 hot experts"),
+}
+HOT_BIAS = 0.23  # bias tilt that sends about a quarter of the selections to 8 hot experts
+
+
+def build_layers(n_layers, seed, device, kind="glm5"):
     import numpy as np  # noqa: F401
     from exl3_amd import synth
     from exl3_amd.moe import DeviceMoeLayer, trellis_words_torch
 
-    cfg = synth.config_glm5()
+    cfg = synth.config_glm5() if kind == "glm5" else synth.config_prefill()
     H, I, E = cfg.hidden, cfg.inter, cfg.n_experts
+    hot = list(range(0, E, E // 8)) if kind == "prefill" else []
     out = []
     for li in range(n_layers):
         tag = f"bench.layer{li}"
+        bias = synth.normal_f32(seed, f"{tag}.gate.e_score_correction_bias", (E,), 0, cfg.bias_std)
+        if hot:
+            bias = bias.copy()
+            bias[hot] += np.float32(HOT_BIAS)
         layer = synth.MoeLayer(cfg, [], None,
                                synth.normal_f16(seed, f"{tag}.gate.weight", (E, H), 0, cfg.router_std),
-                               synth.normal_f32(seed, f"{tag}.gate.e_score_correction_bias", (E,), 0,
-                                                cfg.bias_std))
+                               bias)
         words = {}
         for e in range(E):
             for j, (nm, i_f, o_f, K, cb) in enumerate((("gate_proj", H, I, cfg.gate_up_K, cfg.gate_up_cb),
@@ -70,11 +90,32 @@ def build_layers(n_layers, seed, device):
                     i_f, o_f, suh=synth.normal_f16(seed, p + ".suh", (i_f,), 1, 0.05),
                     svh=synth.normal_f16(seed, p + ".svh", (o_f,), 1, 0.05), K=K, cb=cb))
                 words[3 * e + j] = trellis_words_torch(seed, p + ".trellis", i_f, o_f, K, device)
-        layer.shared = [synth.make_dense_linear(seed, f"{tag}.shared_experts.gate_proj", H, cfg.shared_inter),
-                        synth.make_dense_linear(seed, f"{tag}.shared_experts.up_proj", H, cfg.shared_inter),
-                        synth.make_dense_linear(seed, f"{tag}.shared_experts.down_proj", cfg.shared_inter, H)]
+        SI = cfg.shared_inter
+        dims = ((f"{tag}.shared_experts.gate_proj", H, SI), (f"{tag}.shared_experts.up_proj", H, SI),
+                (f"{tag}.shared_experts.down_proj", SI, H))
+        if cfg.shared_K == 0:
+            layer.shared = [synth.make_dense_linear(seed, p, i_f, o_f) for p, i_f, o_f in dims]
+        else:
+            layer.shared = []
+            for j, (p, i_f, o_f) in enumerate(dims):
+                layer.shared.append(synth.Linear(
+                    i_f, o_f, suh=synth.normal_f16(seed, p + ".suh", (i_f,), 1, 0.05),
+                    svh=synth.normal_f16(seed, p + ".svh", (o_f,), 1, 0.05), K=cfg.shared_K,
+                    cb=cfg.shared_cb))
+                words[("shared", j)] = trellis_words_torch(seed, p + ".trellis", i_f, o_f, cfg.shared_K,
+                                                           device)
         out.append((layer, words, DeviceMoeLayer(layer, device, words=words)))
     return cfg, out
+
+
+def make_inputs(workload, seed, li, B, H):
+    import numpy as np
+    from exl3_amd import synth
+    if workload == "glm5_moe_staged_b64":
+        same = synth.activations(seed, f"bench.same{li}", 1, H)
+        rest = synth.activations(seed, f"bench.rest{li}", B - 48, H)
+        return np.concatenate([np.repeat(same, 48, 0), rest], 0)
+    return synth.activations(seed, f"bench.x{li}", B, H)
 
 
 def cpu_baseline(layer, words, h_list, budget_s):
@@ -117,10 +158,13 @@ def cpu_baseline(layer, words, h_list, budget_s):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--layers", type=int, default=8, help="distinct layer instances rotated")
-    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="glm5_moe_decode_b8",
+                    help="the bench line's workload (default: the metric's B=8 decode); the "
+                         "others are measurement runs of configs[3] and configs[4]")
+    ap.add_argument("--steps", type=int, default=None, help="default 400 (prefill: 20)")
+    ap.add_argument("--warmup", type=int, default=None, help="default 40 (prefill: 3)")
+    ap.add_argument("--layers", type=int, default=None,
+                    help="distinct layer instances rotated (default 8; prefill: 2)")
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -138,11 +182,16 @@ def main():
     import torch
     from exl3_amd import synth
 
+    kind, B, _ = WORKLOADS[args.workload]
+    prefill = kind == "prefill"
+    args.steps = args.steps if args.steps is not None else (20 if prefill else 400)
+    args.warmup = args.warmup if args.warmup is not None else (3 if prefill else 40)
+    args.layers = args.layers if args.layers is not None else (2 if prefill else 8)
     dev = torch.device("cuda:0")
     t0 = time.time()
-    cfg, layers = build_layers(args.layers, args.seed, dev)
-    B, H = args.batch, cfg.hidden
-    xs = [torch.from_numpy(synth.activations(args.seed, f"bench.x{li}", B, H).view(np.float16))
+    cfg, layers = build_layers(args.layers, args.seed, dev, kind)
+    H = cfg.hidden
+    xs = [torch.from_numpy(make_inputs(args.workload, args.seed, li, B, H).view(np.float16))
           .to(dev).view(B, 1, H) for li in range(args.layers)]
     outs = [torch.empty_like(x) for x in xs]
     wss = [d.workspace(B) for _, _, d in layers]
@@ -180,7 +229,7 @@ def main():
     for _, _, d in layers:
         d.timing_reset()
         d.timing_enable(True)
-    for i in range(args.layers * 8):
+    for i in range(args.layers * (2 if prefill else 8)):
         step(i)
     torch.cuda.synchronize()
     tm = {k: 0.0 for k in ("calls", "router_ms", "gate_up_ms", "down_ms", "combine_ms", "total_ms",
@@ -199,8 +248,16 @@ def main():
     routed_gbps = (gu_bytes + dn_bytes) / ((gu_ms + dn_ms) * 1e-3) / 1e9
     distinct = (gu_bytes + dn_bytes) / 6815744.0
 
+    # f16 MFMA work of the routed gate/up launch: 2 flops per weight and routed pair
+    gu_flops = 2.0 * 2 * H * cfg.inter * B * cfg.top_k
+    gu_tflops = gu_flops / (gu_ms * 1e-3) / 1e12
+    shared = ("fp16 1024" if cfg.shared_K == 0 else f"K{cfg.shared_K} trellis {cfg.shared_inter}")
+    cbn = {0: "3inst", 1: "mcg", 2: "mul1"}
+    metric = ("MoE-layer decode tokens/s + achieved HBM GB/s on trellis bytes, B=8, 1 MI355X"
+              if args.workload == "glm5_moe_decode_b8" else
+              f"MoE-layer tokens/s + achieved HBM GB/s on trellis bytes, {args.workload}, 1 MI355X")
     line = {
-        "metric": "MoE-layer decode tokens/s + achieved HBM GB/s on trellis bytes, B=8, 1 MI355X",
+        "metric": metric,
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -212,18 +269,19 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": "glm5_moe_decode_b8", "batch": B, "hidden": H,
+        "config": {"workload": args.workload, "batch": B, "hidden": H,
                    "moe_intermediate": cfg.inter, "experts": cfg.n_experts, "top_k": cfg.top_k,
-                   "gate_up": "K4 mcg", "down": "K5 mcg", "shared_expert": "fp16 1024",
+                   "gate_up": f"K{cfg.gate_up_K} {cbn[cfg.gate_up_cb]}",
+                   "down": f"K{cfg.down_K} {cbn[cfg.down_cb]}", "shared_expert": shared,
                    "layer_instances": args.layers, "parallelism": "none (one GPU)"},
         "roofline": {"kernel": "k_moe_gate_up", "bound": "hbm", "achieved": round(gu_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": measured_traffic("k_moe_gate_up"),
+                     "traffic": measured_traffic("k_moe_gate_up") if args.workload == "glm5_moe_decode_b8" else None,
                      "algorithmic_bytes_per_launch": round(gu_bytes),
                      "avg_launch_ms": round(gu_ms, 5)},
         "roofline_down": {"kernel": "k_moe_down", "achieved": round(dn_gbps, 1),
                           "frac": round(dn_gbps / HBM_PEAK_GBPS, 4),
-                          "traffic": measured_traffic("k_moe_down"),
+                          "traffic": measured_traffic("k_moe_down") if args.workload == "glm5_moe_decode_b8" else None,
                           "algorithmic_bytes_per_launch": round(dn_bytes), "avg_launch_ms": round(dn_ms, 5)},
         "routed_trellis_GBps": round(routed_gbps, 1),
         "distinct_experts_per_step": round(distinct, 2),
@@ -231,6 +289,16 @@ def main():
                                                            "combine_ms", "total_ms")},
         "gpu_ms_per_step_events": round(gpu_ms / args.steps, 5),
     }
+    if prefill:
+        # prefill streams every expert once and is compute-heavy: the MFMA roofline of the
+        # routed gate/up launch (f16 dense peak) next to its HBM one
+        line["roofline"] = {"kernel": "k_moe_gate_up", "bound": "mfma", "achieved": round(gu_tflops, 2),
+                            "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(gu_tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                            "algorithmic_flops_per_launch": gu_flops, "avg_launch_ms": round(gu_ms, 5),
+                            "hbm_GBps": round(gu_gbps, 1), "hbm_frac": round(gu_gbps / HBM_PEAK_GBPS, 4)}
+    if args.workload != "glm5_moe_decode_b8":
+        args.no_cpu_baseline = True  # the CPU leg is sampled on the metric's workload only
     if not args.no_cpu_baseline:
         layer, words, _ = layers[0]
         h_list = [synth.activations(args.seed, f"bench.cpu.x{i}", B, H) for i in range(8)]

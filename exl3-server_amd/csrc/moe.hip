@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -28,6 +29,7 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
                               int shared_mode, bool dense, hipStream_t st);
 int moe_slices(int in);
 exl3_status launch_moe_act(const MoeArgs &a, int shared_mode, int dense_blocks, hipStream_t st);
+exl3_status launch_moe_rotate(const MoeArgs &a, bool shared_trellis, hipStream_t st);
 }
 
 namespace {
@@ -107,10 +109,12 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
 
-// L2. Routing + dispatch, one workgroup.
+// L2. Routing + dispatch. mode bit 0: top-k routing of rows blockIdx.x*16 + wave,
+// strided by the grid; bit 1: the dispatch (one workgroup, after the routing of every
+// row: the same workgroup's or an earlier launch's).
 template <int kJ>
 __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int32_t *id_out,
-                                                    int do_dispatch) {
+                                                    int mode) {
   __shared__ float s_buf[16][kMaxE];  // group path: scores_for_choice per wave; dispatch: counts
   __shared__ int s_keep[16][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -121,7 +125,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
 
   const int jn = (E + 63) / 64;
   const int S = a.logit_splits;  // 0: plain logits (N, E); else S partials in (N, E, 8)
-  for (int b = wave; b < a.N; b += 16) {
+  for (int b = (mode & 1) ? blockIdx.x * 16 + wave : a.N; b < a.N; b += 16 * gridDim.x) {
     // all logit partial and bias loads first (clamped addresses, so no branches split
     // them), then the split sums in split order, the sigmoid and the biased score
     float sc[kJ], sfc[kJ];
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       id_out[(int64_t)b * K + lane] = my_id;
     }
   }
-  if (!do_dispatch) return;
+  if (!(mode & 2)) return;
   __syncthreads();
 
   // Stable counting sort of the P = N*K pairs by expert (pair order b*K + k), the
@@ -356,7 +360,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
 // svh words are all loaded before the first output Hadamard, so a row costs a few
 // memory round trips instead of a few per rank.
 constexpr int kCombineBatch = 8;
-constexpr int kCombineSlices = 4;  // down slices loaded at once (intermediate <= 2048)
+constexpr int kCombineSlices = 2;  // down slices loaded at once (intermediate <= 1024)
 
 __device__ __forceinline__ void down_out(float2 y, uint32_t sv, float &y0, float &y1) {
   y0 = y.x;
@@ -510,9 +514,21 @@ struct MoeLayout {
   size_t total;
   size_t logits, weights, ids, sorted_row, sorted_rank, slot_e, slot, run_expert, run_off, run_len,
       n_runs, pass_expert, pass_off, pass_len, n_passes;
-  size_t yhat_gu, act, yhat_dn, dsh_gu, dsh_act, dsh_dn;
+  size_t yhat_gu, act, yhat_dn, dsh_gu, dsh_act, dsh_dn, xrot;
   int P, R, Imax, S_dn, max_passes;
 };
+
+// Calls of at least this many token rows take the long-run expert kernels (outputs are
+// bit-identical either way): EXL3_MOE_LONG_ROWS, read once, default 65 (at 64 rows the
+// slice-parallel short-run kernels are still faster).
+int64_t long_min_rows() {
+  static const int64_t v = [] {
+    const char *e = std::getenv("EXL3_MOE_LONG_ROWS");
+    const long long x = e ? std::atoll(e) : 0;
+    return x > 0 ? (int64_t)x : (int64_t)65;
+  }();
+  return v;
+}
 
 MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   MoeLayout m{};
@@ -551,6 +567,7 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.dsh_gu = take(dense ? 4 * (size_t)2 * N * SI * kDenseSlots : 0);
   m.dsh_act = take(dense ? 2 * (size_t)N * SI : 0);
   m.dsh_dn = take(dense ? 4 * (size_t)N * H * kDenseSlots : 0);
+  m.xrot = take(N >= long_min_rows() ? 2 * (size_t)slots * 2 * H : 0);
   m.total = o;
   return m;
 }
@@ -575,7 +592,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.shared_kind = L->shared;
   a.logit_splits = dense_mfma_splits(a.H);
   a.n_logit_blocks = (int)((dense_mfma_tasks(N, a.H, a.E) + 3) / 4);
-  a.fold = N > 16;  // long runs: kLongRows-row passes, slices folded in the workgroup
+  a.fold = N >= long_min_rows();  // long runs: kLongRows-row passes, slices folded
   a.pass_rows = (int)std::min<int64_t>(N, 16);
   a.h = h;
   a.router_w = L->router_w;
@@ -604,6 +621,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.dsh_gu = (float *)(ws + m.dsh_gu);
   a.dsh_act = (uint16_t *)(ws + m.dsh_act);
   a.dsh_dn = (float *)(ws + m.dsh_dn);
+  a.xrot = (uint16_t *)(ws + m.xrot);
   a.out = out;
   return a;
 }
@@ -619,15 +637,31 @@ exl3_status check_linear(const exl3_linear_desc &d, int in, int out, const char 
   return EXL3_OK;
 }
 
+// Routing (+ dispatch): one workgroup for up to kRouteOneWg rows (routing and dispatch
+// in one launch); above that the rows' routing spreads over workgroups of 16 rows and
+// the dispatch follows in a one-workgroup launch.
+constexpr int kRouteOneWg = 64;
+
+void launch_route(const MoeArgs &a, float *w_out, int32_t *id_out, int do_dispatch, hipStream_t st) {
+  with_route_chunks(a.E, [&](auto jn) {
+    constexpr int J = decltype(jn)::value;
+    if (a.N <= kRouteOneWg) {
+      k_moe_route<J><<<1, 1024, 0, st>>>(a, w_out, id_out, do_dispatch ? 3 : 1);
+    } else {
+      const unsigned g = (unsigned)std::min<int64_t>((a.N + 15) / 16, 4096);
+      k_moe_route<J><<<g, 1024, 0, st>>>(a, w_out, id_out, 1);
+      if (do_dispatch) k_moe_route<J><<<1, 1024, 0, st>>>(a, w_out, id_out, 2);
+    }
+  });
+}
+
 // L1 + L2: logits, then routing/dispatch. w_out / id_out receive the routing.
 exl3_status launch_logits_route(exl3_moe_layer_s *L, const MoeArgs &a, float *w_out, int32_t *id_out,
                                 int do_dispatch, hipStream_t st) {
   (void)L;
   k_moe_pre<<<a.n_logit_blocks, 256, 0, st>>>(a);
   EXL3_LAUNCHED("k_moe_pre");
-  with_route_chunks(a.E, [&](auto jn) {
-    k_moe_route<decltype(jn)::value><<<1, 1024, 0, st>>>(a, w_out, id_out, do_dispatch);
-  });
+  launch_route(a, w_out, id_out, do_dispatch, st);
   EXL3_LAUNCHED("k_moe_route");
   return EXL3_OK;
 }
@@ -858,9 +892,7 @@ exl3_status exl3_moe_topk_route(const float *logits, const float *bias, int64_t 
   a.router_bias = bias;
   a.logits = const_cast<float *>(logits);
   a.logit_splits = 0;  // plain (N, E) logits
-  with_route_chunks(E, [&](auto jn) {
-    k_moe_route<decltype(jn)::value><<<1, 1024, 0, stream_of(stream)>>>(a, weights, ids, 0);
-  });
+  launch_route(a, weights, ids, 0, stream_of(stream));
   EXL3_LAUNCHED("k_moe_route");
   return EXL3_OK;
 }
@@ -891,6 +923,10 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   // L3: routed gate/up (+ the f16 shared expert's gate/up partials)
   const bool dense_sh = layer->shared == exl3m::kSharedDense;
   const int64_t units = a.fold ? m.max_passes : m.R;  // work units: runs or long-run passes
+  if (a.fold) {
+    rc = launch_moe_rotate(a, layer->shared == exl3m::kSharedTrellis, st);
+    if (rc) return rc;
+  }
   rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, units, a, 0, dense_sh, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[2], st));

@@ -78,6 +78,7 @@ struct MoeArgs {
   float *yhat_gu;      // (P + N, 2, S, Imax): gate/up k-slice partials (S slices of H)
                        // before the output Hadamard
   uint16_t *act;       // (P + N, Imax): rotated SwiGLU output per slot, MFMA k order
+  uint16_t *xrot;      // long-run mode: (P + N, 2, H) f16 rotated gate/up inputs, staged order
   int S_dn;            // slot stride of yhat_dn in slices: max(slices(I), slices(SI))
   float *yhat_dn;      // (P + N, S_dn, H): down k-slice partials per slot, before the
                        // output Hadamard (slots P.. = a trellis shared expert)

@@ -195,6 +195,7 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8
 using exl3m::kLongBlocks;
 using exl3m::kLongRows;
 constexpr int kLongThreads = 512;
+constexpr int kStageBatch = 4;  // staging loads in flight per lane
 
 // Work unit u of the long-run kernels: pass u of the dispatch's pass table, or (shared
 // mode) rows [u * kLongRows, u * kLongRows + kLongRows) of the trellis shared expert.
@@ -243,30 +244,35 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   if (!pass_info(a, u, shared_mode, ri)) return;
   const exl3m::ExpertTab &tb = a.tab[ri.e];
   const uint32_t *base = tb.tr[proj];
-  const uint16_t *suh = tb.suh[proj];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int np = cb * kWaves + wave;
   const bool active = np < n_np;  // idle waves still stage rows and meet the barriers
   const int slice_k = kStepTiles * ss * 16;
-  const int nblk = slice_k / 128;
   const int xs_stride = slice_k / 2;
   uint32_t *xs = smem;
   u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * kSlotChunks;
 
+  const int q_row = xs_stride / 4;  // 16-byte chunks per staged row
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
     f32x4 acc[kLongBlocks][2];
     for (int sl = 0; sl < n_sl; ++sl) {
-      const int k_base = sl * slice_k;
-      for (int bi = wave; bi < nr * nblk; bi += kWaves) {
-        const int r = bi / nblk, blk = bi % nblk;
-        const int row = a.sorted_row[ri.off + p0 + r];
-        const int kc = k_base + blk * 128 + 2 * lane;
-        const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
-        const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
-        float v0 = lo16(hx), v1 = hi16(hx);
-        wave_had_pre(v0, v1, lo16(sx), hi16(sx));
-        stage_pair(xs + r * xs_stride, blk, lane, pack16(v0, v1));
+      // the slice of the pass's rows, already rotated by k_moe_rotate (x_rot rows of
+      // this projection, in the staged k order)
+      const int items = nr * q_row;
+      for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatch) {
+        uint4 c[kStageBatch];
+#pragma unroll
+        for (int q = 0; q < kStageBatch; ++q) {
+          const int i = min(i0 + q * kLongThreads, items - 1);
+          c[q] = reinterpret_cast<const uint4 *>(
+              a.xrot + ((int64_t)(ri.off + p0 + i / q_row) * 2 + proj) * a.H + sl * slice_k)[i % q_row];
+        }
+#pragma unroll
+        for (int q = 0; q < kStageBatch; ++q) {
+          const int i = i0 + q * kLongThreads;
+          if (i < items) reinterpret_cast<uint4 *>(xs + (i / q_row) * xs_stride)[i % q_row] = c[q];
+        }
       }
       __syncthreads();
       if (active) {
@@ -323,10 +329,20 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
     const int nr = min(kLongRows, ri.len - p0);
     f32x4 acc[kLongBlocks][2];
     for (int sl = 0; sl < n_sl; ++sl) {
-      for (int i = threadIdx.x; i < nr * q_row; i += kLongThreads) {
-        const int r = i / q_row, q = i % q_row;
-        reinterpret_cast<uint4 *>(xs + r * xs_stride)[q] = reinterpret_cast<const uint4 *>(
-            a.act + (int64_t)(ri.off + p0 + r) * a.Imax + sl * slice_k)[q];
+      const int items = nr * q_row;  // 16-byte chunks of the slice's rows
+      for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatch) {
+        uint4 c[kStageBatch];
+#pragma unroll
+        for (int q = 0; q < kStageBatch; ++q) {
+          const int i = min(i0 + q * kLongThreads, items - 1);
+          c[q] = reinterpret_cast<const uint4 *>(a.act + (int64_t)(ri.off + p0 + i / q_row) * a.Imax +
+                                                 sl * slice_k)[i % q_row];
+        }
+#pragma unroll
+        for (int q = 0; q < kStageBatch; ++q) {
+          const int i = i0 + q * kLongThreads;
+          if (i < items) reinterpret_cast<uint4 *>(xs + (i / q_row) * xs_stride)[i % q_row] = c[q];
+        }
       }
       __syncthreads();
       if (active) {
@@ -352,6 +368,29 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
         }
     }
   }
+}
+
+// Long-run mode: the input Hadamard of every (slot, projection) once, x_rot[slot][proj]
+// = had_pre(h[row], suh of the slot's expert and projection) in the staged k order, so
+// the gate/up workgroups of a pass (one per 256 output columns) copy it instead of each
+// rotating it again. One wave per (slot, projection, 128-block); slots [0, n_slots):
+// routed slots, then (trellis shared expert) the N shared slots.
+__global__ __launch_bounds__(256) void k_moe_rotate(MoeArgs a, int n_slots) {
+  const int lane = threadIdx.x & 63;
+  const int nblk = a.H / 128;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gw >= (int64_t)n_slots * 2 * nblk) return;
+  const int blk = (int)(gw % nblk);
+  const int proj = (int)((gw / nblk) & 1);
+  const int64_t slot = gw / (2 * nblk);
+  const int e = slot < a.P ? a.slot_e[slot] : a.E;
+  const int row = a.sorted_row[slot];
+  const int kc = blk * 128 + 2 * lane;
+  const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
+  const uint32_t sx = *reinterpret_cast<const uint32_t *>(a.tab[e].suh[proj] + kc);
+  float v0 = lo16(hx), v1 = hi16(hx);
+  wave_had_pre(v0, v1, lo16(sx), hi16(sx));
+  stage_pair(reinterpret_cast<uint32_t *>(a.xrot + (slot * 2 + proj) * a.H), blk, lane, pack16(v0, v1));
 }
 
 // One wave per (slot, 128-block of the intermediate): the gate/up slice partials
@@ -438,8 +477,9 @@ template <typename Kern>
 static exl3_status launch_kernel(Kern k, unsigned blocks, unsigned threads, size_t lds, hipStream_t st,
                                  const MoeArgs &a, int shared_mode, int dense_blocks, bool &attr_set) {
   if (!attr_set) {
+    // above the 64 KB default; leaves room for the kernels' static LDS
     EXL3_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 160 * 1024));
+                                 128 * 1024));
     attr_set = true;
   }
   k<<<blocks, threads, lds, st>>>(a, shared_mode, dense_blocks);
@@ -452,12 +492,16 @@ static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeA
                           int shared_mode, int dense_blocks) {
   const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
   if (a.fold) {
-    const size_t lds = expert_lds(in, kLongRows, kLongThreads / 64);
-    static bool set_gu = false, set_dn = false;
-    return which == 0 ? launch_kernel(k_moe_gate_up_long<K, CB, PD>, blocks, kLongThreads, lds, st, a,
-                                      shared_mode, dense_blocks, set_gu)
-                      : launch_kernel(k_moe_down_long<K, CB, PD>, blocks, kLongThreads, lds, st, a,
-                                      shared_mode, dense_blocks, set_dn);
+    if constexpr (PD <= 2) {  // long-run kernels keep at most 2 steps in flight (VGPRs)
+      const size_t lds = expert_lds(in, kLongRows, kLongThreads / 64);
+      static bool set_gu = false, set_dn = false;
+      return which == 0 ? launch_kernel(k_moe_gate_up_long<K, CB, PD>, blocks, kLongThreads, lds, st,
+                                        a, shared_mode, dense_blocks, set_gu)
+                        : launch_kernel(k_moe_down_long<K, CB, PD>, blocks, kLongThreads, lds, st, a,
+                                        shared_mode, dense_blocks, set_dn);
+    } else {
+      return fail(EXL3_ERR_INVALID, "long-run expert kernels take at most 2 steps in flight");
+    }
   }
   static bool set_gu = false, set_dn = false;
   return which == 0
@@ -501,6 +545,8 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
   const int out = which == 0 ? (shared_mode ? a.SI : a.I) : a.H;
   const int n_sl = n_slices(in / 16);
   const int waves = a.fold ? kLongThreads / 64 : kGuThreads / 64;
+  if (expert_lds(in, a.fold ? kLongRows : a.pass_rows, waves) > 128 * 1024)
+    return fail(EXL3_ERR_UNSUPPORTED, "expert kernel LDS above 128 KB");
   int64_t blocks;
   if (a.fold)
     blocks = runs * (which == 0 ? 2 : 1) * ((out / 32 + waves - 1) / waves);
@@ -513,7 +559,7 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
   blocks += dense_blocks;
   if (blocks == 0) return EXL3_OK;
   if (blocks > 0x7fffffff) return fail(EXL3_ERR_UNSUPPORTED, "expert launch too large");
-  const int pd = moe_prefetch(in / 16, K);
+  const int pd = a.fold ? std::min(moe_prefetch(in / 16, K), 2) : moe_prefetch(in / 16, K);
   exl3_status rc = EXL3_OK;
   const unsigned ub = (unsigned)blocks;
 #define EXL3_KC(KK)                                                                            \
@@ -529,6 +575,17 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
 #undef EXL3_KC
   if (rc) return rc;
   EXL3_LAUNCHED(which == 0 ? "k_moe_gate_up" : "k_moe_down");
+  return EXL3_OK;
+}
+
+// Long-run mode: x_rot of the P routed slots and, with a trellis shared expert, the N
+// shared slots.
+exl3_status launch_moe_rotate(const MoeArgs &a, bool shared_trellis, hipStream_t st) {
+  const int64_t n_slots = (int64_t)a.P + (shared_trellis ? a.N : 0);
+  const int64_t waves = n_slots * 2 * (a.H / 128);
+  if (waves == 0) return EXL3_OK;
+  k_moe_rotate<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a, (int)n_slots);
+  EXL3_LAUNCHED("k_moe_rotate");
   return EXL3_OK;
 }
 
