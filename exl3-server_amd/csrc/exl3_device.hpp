@@ -222,6 +222,23 @@ __device__ __forceinline__ void wave_fwht128(float &v0, float &v1) {
 // Round-trip helpers for the two sides of a trellis linear (trellis_gemm.cpp:383-399).
 // pre : xhat = f16( fwht(f32(x) * f32(s)) * scale )
 // post: y    = f16( (fwht(f32(f16(yhat))) * scale) * f32(s) )
+// NB independent 128-blocks at once (their butterfly stages interleaved).
+template <int NB>
+__device__ __forceinline__ void wave_had_pre_n(float (&v0)[NB], float (&v1)[NB],
+                                               const float (&s0)[NB], const float (&s1)[NB]) {
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    v0[i] = v0[i] * s0[i];
+    v1[i] = v1[i] * s1[i];
+  }
+  wave_fwht128_n<NB>(v0, v1);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    v0[i] = f32_rounded(v0[i] * kHadScale);
+    v1[i] = f32_rounded(v1[i] * kHadScale);
+  }
+}
+
 __device__ __forceinline__ void wave_had_pre(float &v0, float &v1, float s0, float s1) {
   v0 = v0 * s0;
   v1 = v1 * s1;

@@ -109,6 +109,74 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
 
+// The dispatch of P <= 64 pairs by one wave (lane i = pair i, its expert in ids[i]):
+// the same stable sort by expert, run table and pass table as the workgroup-wide
+// counting sort. The 64 keys (expert, pair index) are sorted across the lanes by a
+// bitonic network (21 compare-exchange stages over lane exchanges), after which lane
+// p holds the pair at sorted position p; runs start where the expert changes.
+static_assert(64 < 2 * (kLongRows + 1), "at most one run of 64 pairs exceeds a pass");
+
+template <int J>
+__device__ __forceinline__ uint32_t bitonic_step(uint32_t key, int k) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t other = __builtin_bit_cast(uint32_t, xor_lanes<J>(__builtin_bit_cast(float, key)));
+  const bool keep_min = ((lane & J) == 0) == ((lane & k) == 0);
+  return keep_min ? min(key, other) : max(key, other);
+}
+
+__device__ __forceinline__ void dispatch_small(const MoeArgs &a, const int *ids) {
+  const int lane = threadIdx.x & 63;
+  const int P = a.P, K = a.topk;
+  uint32_t key = lane < P ? (((uint32_t)ids[lane] << 6) | (uint32_t)lane) : 0xFFFFFFFFu;
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1) {
+    if (k >= 64) key = bitonic_step<32>(key, k);
+    if (k >= 32) key = bitonic_step<16>(key, k);
+    if (k >= 16) key = bitonic_step<8>(key, k);
+    if (k >= 8) key = bitonic_step<4>(key, k);
+    if (k >= 4) key = bitonic_step<2>(key, k);
+    key = bitonic_step<1>(key, k);
+  }
+  // lane p: sorted position p
+  const bool valid = lane < P;
+  const int se = (int)(key >> 6), pair = (int)(key & 63u);
+  if (valid) {
+    a.sorted_row[lane] = pair / K;
+    a.sorted_rank[lane] = pair % K;
+    a.slot_e[lane] = se;
+    a.slot[pair] = lane;
+  }
+  const int prev = __shfl(se, lane > 0 ? lane - 1 : 0, 64);
+  const bool start = valid && (lane == 0 || prev != se);
+  const uint64_t starts = __ballot(start);
+  const uint64_t upto = lanes_below() | (1ull << lane);
+  const int run_i = __builtin_popcountll(starts & upto) - 1;
+  const uint64_t later = starts & ~upto;
+  const int run_end = later ? __builtin_ctzll(later) : P;
+  const int len = run_end - lane;
+  // passes of <= kLongRows rows: with P <= 64 only one run can need two
+  const uint64_t big = __ballot(start && len > kLongRows);
+  const int pass_i = run_i + (big && __builtin_ctzll(big) < lane ? 1 : 0);
+  if (start) {
+    a.run_expert[run_i] = se;
+    a.run_off[run_i] = lane;
+    a.run_len[run_i] = len;
+    for (int q = 0; q * kLongRows < len; ++q) {
+      a.pass_expert[pass_i + q] = se;
+      a.pass_off[pass_i + q] = lane + q * kLongRows;
+      a.pass_len[pass_i + q] = min(kLongRows, len - q * kLongRows);
+    }
+  }
+  if (lane == 0) {
+    *a.n_runs = __builtin_popcountll(starts);
+    *a.n_passes = __builtin_popcountll(starts) + (big ? 1 : 0);
+  }
+  for (int i = lane; i < a.N; i += 64) {
+    a.sorted_row[P + i] = i;
+    a.sorted_rank[P + i] = 0;
+  }
+}
+
 // L2. Routing + dispatch. mode bit 0: top-k routing of rows blockIdx.x*16 + wave,
 // strided by the grid; bit 1: the dispatch (one workgroup, after the routing of every
 // row: the same workgroup's or an earlier launch's).
@@ -117,6 +185,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
                                                     int mode) {
   __shared__ float s_buf[16][kMaxE];  // group path: scores_for_choice per wave; dispatch: counts
   __shared__ int s_keep[16][64];
+  __shared__ int s_small[64];         // the pairs' experts when P <= 64 (one-wave dispatch)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = a.E, K = a.topk;
   const int ng = a.n_group > 1 ? a.n_group : 1;
@@ -227,7 +296,15 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
         }
       }
       const uint32_t mkey = wave_max_u32(bkey);
-      const uint32_t ewin = wave_min_u32(bkey == mkey && bkey != 0 ? (uint32_t)(lane + 64 * bj) : 0xFFFFFFFFu);
+      // the lane holding the maximum; on a tie between lanes, the lowest expert id
+      const uint64_t hold = __ballot(bkey == mkey && bkey != 0);
+      uint32_t ewin;
+      if (__builtin_popcountll(hold) == 1) {
+        const int hl = __builtin_ctzll(hold);
+        ewin = (uint32_t)(hl + 64 * __builtin_amdgcn_readlane(bj, hl));
+      } else {
+        ewin = wave_min_u32(bkey == mkey && bkey != 0 ? (uint32_t)(lane + 64 * bj) : 0xFFFFFFFFu);
+      }
       const int wl = (int)(ewin & 63u);
       const float bs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bsc), wl));
       if (lane == wl) taken |= 1u << (ewin >> 6);
@@ -243,10 +320,15 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       w = w * a.routed_scaling_factor;
       w_out[(int64_t)b * K + lane] = w;
       id_out[(int64_t)b * K + lane] = my_id;
+      if ((mode & 2) && b * K + lane < 64) s_small[b * K + lane] = my_id;
     }
   }
   if (!(mode & 2)) return;
   __syncthreads();
+  if (a.P <= 64) {
+    if (wave == 0) dispatch_small(a, s_small);
+    return;
+  }
 
   // Stable counting sort of the P = N*K pairs by expert (pair order b*K + k), the
   // order of the reference's stable_sort (glm5_moe.cpp:191-200).

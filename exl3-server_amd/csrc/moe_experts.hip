@@ -373,24 +373,42 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
 // Long-run mode: the input Hadamard of every (slot, projection) once, x_rot[slot][proj]
 // = had_pre(h[row], suh of the slot's expert and projection) in the staged k order, so
 // the gate/up workgroups of a pass (one per 256 output columns) copy it instead of each
-// rotating it again. One wave per (slot, projection, 128-block); slots [0, n_slots):
-// routed slots, then (trellis shared expert) the N shared slots.
+// rotating it again. One wave per (slot, projection), kRotBatch 128-blocks at a time;
+// slots [0, n_slots): routed slots, then (trellis shared expert) the N shared slots.
+constexpr int kRotBatch = 8;
+
 __global__ __launch_bounds__(256) void k_moe_rotate(MoeArgs a, int n_slots) {
   const int lane = threadIdx.x & 63;
   const int nblk = a.H / 128;
   const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (gw >= (int64_t)n_slots * 2 * nblk) return;
-  const int blk = (int)(gw % nblk);
-  const int proj = (int)((gw / nblk) & 1);
-  const int64_t slot = gw / (2 * nblk);
+  if (gw >= (int64_t)n_slots * 2) return;
+  const int proj = (int)(gw & 1);
+  const int64_t slot = gw >> 1;
   const int e = slot < a.P ? a.slot_e[slot] : a.E;
-  const int row = a.sorted_row[slot];
-  const int kc = blk * 128 + 2 * lane;
-  const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
-  const uint32_t sx = *reinterpret_cast<const uint32_t *>(a.tab[e].suh[proj] + kc);
-  float v0 = lo16(hx), v1 = hi16(hx);
-  wave_had_pre(v0, v1, lo16(sx), hi16(sx));
-  stage_pair(reinterpret_cast<uint32_t *>(a.xrot + (slot * 2 + proj) * a.H), blk, lane, pack16(v0, v1));
+  const uint16_t *hrow = a.h + (int64_t)a.sorted_row[slot] * a.H + 2 * lane;
+  const uint16_t *suh = a.tab[e].suh[proj] + 2 * lane;
+  uint32_t *out = reinterpret_cast<uint32_t *>(a.xrot + (slot * 2 + proj) * a.H);
+  for (int b0 = 0; b0 < nblk; b0 += kRotBatch) {
+    uint32_t hx[kRotBatch], sx[kRotBatch];
+#pragma unroll
+    for (int q = 0; q < kRotBatch; ++q) {
+      const int blk = min(b0 + q, nblk - 1);
+      hx[q] = *reinterpret_cast<const uint32_t *>(hrow + blk * 128);
+      sx[q] = *reinterpret_cast<const uint32_t *>(suh + blk * 128);
+    }
+    float v0[kRotBatch], v1[kRotBatch], s0[kRotBatch], s1[kRotBatch];
+#pragma unroll
+    for (int q = 0; q < kRotBatch; ++q) {
+      v0[q] = lo16(hx[q]);
+      v1[q] = hi16(hx[q]);
+      s0[q] = lo16(sx[q]);
+      s1[q] = hi16(sx[q]);
+    }
+    wave_had_pre_n<kRotBatch>(v0, v1, s0, s1);
+#pragma unroll
+    for (int q = 0; q < kRotBatch; ++q)
+      if (b0 + q < nblk) stage_pair(out, b0 + q, lane, pack16(v0[q], v1[q]));
+  }
 }
 
 // One wave per (slot, 128-block of the intermediate): the gate/up slice partials
@@ -582,7 +600,7 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
 // shared slots.
 exl3_status launch_moe_rotate(const MoeArgs &a, bool shared_trellis, hipStream_t st) {
   const int64_t n_slots = (int64_t)a.P + (shared_trellis ? a.N : 0);
-  const int64_t waves = n_slots * 2 * (a.H / 128);
+  const int64_t waves = n_slots * 2;
   if (waves == 0) return EXL3_OK;
   k_moe_rotate<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a, (int)n_slots);
   EXL3_LAUNCHED("k_moe_rotate");

@@ -240,6 +240,10 @@ def test_glm5_layer_b8_vs_oracle(oracle, dev):
     rel, cos = check_out(y, want)
     dg = d.diag()
     assert dg["calls"] == 1 and dg["pairs"] == 64 and dg["distinct_experts"] == len(used)
+    hist = {}
+    for r in oracle.moe_runs(idx)["run_len"].tolist():
+        hist[min(r, 64)] = hist.get(min(r, 64), 0) + 1
+    assert dg["run_hist"] == hist
     print(f"\nglm5 B=8: distinct experts {len(used)}, max|err|/rms {rel:.3g}, cos {cos:.7f}, "
           f"near-tie flips {flips}")
     d.close()
