@@ -48,6 +48,10 @@ __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 
 constexpr int kGuThreads = 256;
 constexpr int kDnThreads = 256;
+// Waves per SIMD the short-run expert kernels are compiled for: 7 (<= 72 VGPRs) where
+// K <= 4 fits without spills, else 6 (<= 80).
+template <int K>
+constexpr int kExpertWaves = K <= 4 ? 7 : 6;
 
 struct RunInfo {
   int e, off, len;
@@ -73,7 +77,7 @@ __device__ __forceinline__ bool run_info(const MoeArgs &a, int u, int shared_mod
 // the slice's 128-blocks into LDS, then one slice per wave, raw f32 partials to yhat_gu
 // (summed in slice order by k_moe_act).
 template <int K, int CB, int PD>
-__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_blocks) {
+__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExpertWaves<K>, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
   if ((int)blockIdx.x < dense_blocks) {
     shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu, blockIdx.x,
@@ -102,8 +106,11 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8
   uint32_t *xs = smem;
   u32x4 *slot = reinterpret_cast<u32x4 *>(smem + a.pass_rows * xs_stride) + wave * kSlotChunks;
 
+  SliceStream<K, PD> S;
   for (int p0 = 0; p0 < ri.len; p0 += a.pass_rows) {
     const int nr = min(a.pass_rows, ri.len - p0);
+    // the slice's first ring words are in flight while the rows are staged
+    S.start(base, k_tiles, out / 16, sl * kStepTiles * ss, cb * 4 + wave);
     for (int bi = wave; bi < nr * nblk; bi += kGuThreads / 64) {
       const int r = bi / nblk, blk = bi % nblk;
       const int row = a.sorted_row[ri.off + p0 + r];
@@ -116,8 +123,7 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8
     }
     __syncthreads();
     f32x4 D0, D1;
-    qmv_slice<K, CB, PD>(base, k_tiles, out / 16, sl * kStepTiles * ss, cb * 4 + wave, ss,
-                         xs + min(lane & 15, nr - 1) * xs_stride, slot, D0, D1);
+    qmv_slice_run<K, CB, PD>(S, ss, xs + min(lane & 15, nr - 1) * xs_stride, slot, D0, D1);
     const int col = cb * 128 + wave * 32;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -138,7 +144,7 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(6, 8
 // per wave, raw f32 partials to yhat_dn (the output Hadamard and the routing weight
 // are applied by k_moe_combine).
 template <int K, int CB, int PD>
-__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_blocks) {
+__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExpertWaves<K>, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
   if ((int)blockIdx.x < dense_blocks) {
     shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn, blockIdx.x, kDnThreads / 64);
@@ -160,8 +166,10 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8
   uint32_t *xs = smem;
   u32x4 *slot = reinterpret_cast<u32x4 *>(smem + a.pass_rows * xs_stride) + wave * kSlotChunks;
 
+  SliceStream<K, PD> S;
   for (int p0 = 0; p0 < ri.len; p0 += a.pass_rows) {
     const int nr = min(a.pass_rows, ri.len - p0);
+    S.start(tb.tr[2], k_tiles, a.H / 16, sl * kStepTiles * ss, cb * 4 + wave);
     const int q_row = xs_stride / 4;  // 16-byte chunks per staged row
     for (int i = threadIdx.x; i < nr * q_row; i += kDnThreads) {
       const int r = i / q_row, q = i % q_row;
@@ -170,8 +178,7 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(6, 8
     }
     __syncthreads();
     f32x4 D0, D1;
-    qmv_slice<K, CB, PD>(tb.tr[2], k_tiles, a.H / 16, sl * kStepTiles * ss, cb * 4 + wave, ss,
-                         xs + min(lane & 15, nr - 1) * xs_stride, slot, D0, D1);
+    qmv_slice_run<K, CB, PD>(S, ss, xs + min(lane & 15, nr - 1) * xs_stride, slot, D0, D1);
     const int col = cb * 128 + wave * 32;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

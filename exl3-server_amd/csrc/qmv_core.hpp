@@ -193,30 +193,41 @@ __device__ __forceinline__ StepLane step_lane() {
 // word, (k_tiles, tiles_n) its tile grid; n-pair np covers n-tiles 2np, 2np+1. xrow =
 // this lane's staged activation row (A-operand row l % 16), positioned at the slice's
 // first k-tile; slot = this wave's kSlotChunks-chunk LDS slot. PD = steps in flight
-// (divides nsteps).
+// (divides nsteps). Split in two so that callers can issue the first PD steps' ring
+// loads (SliceStream::start) before staging their activations, and run the slice
+// (qmv_slice_run) once the staged rows are visible.
+template <int K, int PD>
+struct SliceStream {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t vo0, vo1, so0, step_bytes;
+  StepLoads<K> L[PD];
+
+  __device__ __forceinline__ void start(const uint32_t *base, int k_tiles, int tiles_n, int kt0, int np) {
+    constexpr uint32_t kTileBytes = 32 * K;
+    constexpr int kChunks = 16 * K, kRowChunks = 4 * K;
+    const int lane = threadIdx.x & 63;
+    rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0,
+                                             (int)((uint32_t)k_tiles * tiles_n * kTileBytes), 0x00020000);
+    step_bytes = (uint32_t)kStepTiles * tiles_n * kTileBytes;
+    auto chunk_off = [&](int c) -> uint32_t {
+      return c < kChunks ? ((uint32_t)(c / kRowChunks) * tiles_n + 2 * np) * kTileBytes +
+                               (uint32_t)(c % kRowChunks) * 16
+                         : kNoChunk;
+    };
+    vo0 = chunk_off(lane);
+    vo1 = chunk_off(64 + lane);
+    so0 = (uint32_t)kt0 * tiles_n * kTileBytes;
+#pragma unroll
+    for (int b = 0; b < PD; ++b) step_load<K>(rsrc, vo0, vo1, so0 + b * step_bytes, L[b]);
+  }
+};
+
 template <int K, int CB, int PD>
-__device__ __forceinline__ void qmv_slice(const uint32_t *base, int k_tiles, int tiles_n, int kt0,
-                                          int np, int nsteps, const uint32_t *xrow, u32x4 *slot,
-                                          f32x4 &D0, f32x4 &D1) {
+__device__ __forceinline__ void qmv_slice_run(SliceStream<K, PD> &S, int nsteps, const uint32_t *xrow,
+                                              u32x4 *slot, f32x4 &D0, f32x4 &D1) {
   static_assert(16 * K <= kSlotChunks, "slot size");
   const StepLane sl = step_lane();
-  const int lane = threadIdx.x & 63;
-  constexpr uint32_t kTileBytes = 32 * K;
-  constexpr int kChunks = 16 * K, kRowChunks = 4 * K;
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)base, (short)0, (int)((uint32_t)k_tiles * tiles_n * kTileBytes), 0x00020000);
-  const uint32_t step_bytes = (uint32_t)kStepTiles * tiles_n * kTileBytes;
-  auto chunk_off = [&](int c) -> uint32_t {
-    return c < kChunks ? ((uint32_t)(c / kRowChunks) * tiles_n + 2 * np) * kTileBytes +
-                             (uint32_t)(c % kRowChunks) * 16
-                       : kNoChunk;
-  };
-  const uint32_t vo0 = chunk_off(lane), vo1 = chunk_off(64 + lane);
   const int wbase = (sl.kt * 2 + sl.nt) * 8 * K;  // this lane's tile in the slot, in words
-  const uint32_t so0 = (uint32_t)kt0 * tiles_n * kTileBytes;
-  StepLoads<K> L[PD];
-#pragma unroll
-  for (int b = 0; b < PD; ++b) step_load<K>(rsrc, vo0, vo1, so0 + b * step_bytes, L[b]);
   D0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   D1 = D0;
   // A operand of step s: 32 bytes at k-tile 4s + kt of the row (8 words per k-tile).
@@ -226,8 +237,8 @@ __device__ __forceinline__ void qmv_slice(const uint32_t *base, int k_tiles, int
 #pragma unroll
     for (int b = 0; b < PD; ++b) {
       uint32_t W[K + 1];
-      step_words<K>(slot, wbase, sl.m, L[b], W);
-      step_load<K>(rsrc, vo0, vo1, so0 + (s0 + b + PD) * step_bytes, L[b]);
+      step_words<K>(slot, wbase, sl.m, S.L[b], W);
+      step_load<K>(S.rsrc, S.vo0, S.vo1, S.so0 + (s0 + b + PD) * S.step_bytes, S.L[b]);
       const uint32_t *xs = xa + (s0 + b) * (kStepTiles * 8);
       const f16x8 A0 = *reinterpret_cast<const f16x8 *>(xs);
       const f16x8 A1 = *reinterpret_cast<const f16x8 *>(xs + 4);
@@ -237,12 +248,21 @@ __device__ __forceinline__ void qmv_slice(const uint32_t *base, int k_tiles, int
 #pragma unroll
   for (int b = 0; b < PD; ++b) {
     uint32_t W[K + 1];
-    step_words<K>(slot, wbase, sl.m, L[b], W);
+    step_words<K>(slot, wbase, sl.m, S.L[b], W);
     const uint32_t *xs = xa + (s0 + b) * (kStepTiles * 8);
     const f16x8 A0 = *reinterpret_cast<const f16x8 *>(xs);
     const f16x8 A1 = *reinterpret_cast<const f16x8 *>(xs + 4);
     mfma_step<K, CB>(W, A0, A1, D0, D1);
   }
+}
+
+template <int K, int CB, int PD>
+__device__ __forceinline__ void qmv_slice(const uint32_t *base, int k_tiles, int tiles_n, int kt0,
+                                          int np, int nsteps, const uint32_t *xrow, u32x4 *slot,
+                                          f32x4 &D0, f32x4 &D1) {
+  SliceStream<K, PD> S;
+  S.start(base, k_tiles, tiles_n, kt0, np);
+  qmv_slice_run<K, CB, PD>(S, nsteps, xrow, slot, D0, D1);
 }
 
 // Long runs: RB blocks of 16 token rows share one decode. The four B operands of a
