@@ -479,7 +479,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     }
     const uint16_t *svp[kCombineBatch];
 #pragma unroll
-    for (int j = 0; j < kCombineBatch; ++j) svp[j] = a.tab[e[j]].svh[2];
+    for (int j = 0; j < kCombineBatch; ++j) svp[j] = a.svh_s[2] + (int64_t)e[j] * a.H;
     uint32_t sv[kCombineBatch];
     float2 y[kCombineBatch];
     if (n_sl <= kCombineSlices) {
@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     const float2 ys = exl3m::ordered_sum2<4>(a.yhat_dn + slot * a.S_dn * plane + c, plane,
                                              a.fold ? 1 : n_slices(a.SI / 16));
     float y0, y1;
-    down_out(ys, *reinterpret_cast<const uint32_t *>(a.tab[a.E].svh[2] + c), y0, y1);
+    down_out(ys, *reinterpret_cast<const uint32_t *>(a.svh_s[2] + (int64_t)a.E * a.H + c), y0, y1);
     r0 += y0;
     r1 += y1;
   } else if (a.shared_kind == exl3m::kSharedDense) {
@@ -545,6 +545,25 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(r0)) |
                      ((uint32_t)bitcast<uint16_t>(to_f16(r1)) << 16);
   *reinterpret_cast<uint32_t *>(a.out + (int64_t)row * a.H + c) = o;
+}
+
+// Stacks every expert's suh/svh (entry e of tab) into the layer's scale arrays: block
+// (e, j) copies suh[j] (length in_j) and svh[j] (out_j) of entry e, rows of stride
+// stride_in[j] / stride_out[j]. Entries without a tensor (no shared expert) are skipped.
+struct ScaleGather {
+  uint16_t *suh[3], *svh[3];
+  int len_in[2][3], len_out[2][3];  // [routed, shared][j]
+  int stride_in[3], stride_out[3];
+};
+
+__global__ __launch_bounds__(256) void k_gather_scales(const ExpertTab *tab, int E, ScaleGather g) {
+  const int e = blockIdx.x / 3, j = blockIdx.x % 3;
+  const ExpertTab &t = tab[e];
+  const int sh = e == E ? 1 : 0;
+  if (t.suh[j])
+    for (int i = threadIdx.x; i < g.len_in[sh][j]; i += 256) g.suh[j][(int64_t)e * g.stride_in[j] + i] = t.suh[j][i];
+  if (t.svh[j])
+    for (int i = threadIdx.x; i < g.len_out[sh][j]; i += 256) g.svh[j][(int64_t)e * g.stride_out[j] + i] = t.svh[j][i];
 }
 
 // (in, out) f16 -> (out, in) f16 through a 64x64 LDS tile per workgroup (256 threads);
@@ -579,6 +598,8 @@ struct exl3_moe_layer_s {
   const uint16_t *router_w;
   const float *router_bias;
   ExpertTab *tab_dev;  // E + 1 entries
+  uint16_t *scales;    // stacked suh/svh (MoeArgs::suh_s/svh_s), E + 1 entries each
+  size_t scale_off[6]; // suh 0..2, svh 0..2 (f16 elements)
   std::vector<int64_t> expert_bytes;  // trellis bytes (+ scales) per routed expert
   std::vector<int64_t> gu_bytes, dn_bytes;  // trellis bytes of gate+up / down per expert
   int diag_on;
@@ -680,6 +701,10 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.router_w = L->router_w;
   a.router_bias = L->router_bias;
   a.tab = L->tab_dev;
+  for (int j = 0; j < 3; ++j) {
+    a.suh_s[j] = L->scales + L->scale_off[j];
+    a.svh_s[j] = L->scales + L->scale_off[3 + j];
+  }
   for (int j = 0; j < 3; ++j) a.sh_dense[j] = L->sh_dense_t[j];
   a.logits = (float *)(ws + m.logits);
   a.weights = (float *)(ws + m.weights);
@@ -900,6 +925,51 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
     delete L;
     return hip_check(e1, "hipMemcpy(expert table)");
   }
+  {
+    // stacked scales: suh 0,1 (E+1, H), suh 2 (E+1, Imax), svh 0,1 (E+1, Imax), svh 2 (E+1, H)
+    const int Imax = std::max(I, L->SI);
+    const size_t rows = (size_t)E + 1;
+    const size_t sz[6] = {rows * H, rows * H, rows * Imax, rows * Imax, rows * Imax, rows * H};
+    size_t total = 0;
+    for (int j = 0; j < 6; ++j) {
+      L->scale_off[j] = total;
+      total += align_up(sz[j], 128);
+    }
+    hipError_t e2 = hipMalloc(&L->scales, total * sizeof(uint16_t));
+    if (e2 == hipSuccess) e2 = hipMemset(L->scales, 0, total * sizeof(uint16_t));
+    if (e2 == hipSuccess) {
+      ScaleGather g{};
+      for (int j = 0; j < 3; ++j) {
+        g.suh[j] = L->scales + L->scale_off[j];
+        g.svh[j] = L->scales + L->scale_off[3 + j];
+      }
+      const int SI = L->SI;
+      const int in_r[3] = {H, H, I}, out_r[3] = {I, I, H};
+      const int in_s[3] = {H, H, SI}, out_s[3] = {SI, SI, H};
+      for (int j = 0; j < 3; ++j) {
+        g.len_in[0][j] = in_r[j];
+        g.len_out[0][j] = out_r[j];
+        g.len_in[1][j] = L->shared == 1 ? in_s[j] : 0;
+        g.len_out[1][j] = L->shared == 1 ? out_s[j] : 0;
+      }
+      g.stride_in[0] = H;
+      g.stride_in[1] = H;
+      g.stride_in[2] = Imax;
+      g.stride_out[0] = Imax;
+      g.stride_out[1] = Imax;
+      g.stride_out[2] = H;
+      k_gather_scales<<<(unsigned)(rows * 3), 256, 0, 0>>>(L->tab_dev, E, g);
+      e2 = hipGetLastError();
+      if (e2 == hipSuccess) e2 = hipStreamSynchronize(0);
+    }
+    if (e2 != hipSuccess) {
+      if (L->scales) (void)hipFree(L->scales);
+      (void)hipFree(L->tab_dev);
+      if (L->sh_dense_t[0]) (void)hipFree(L->sh_dense_t[0]);
+      delete L;
+      return hip_check(e2, "stacked scales");
+    }
+  }
   L->diag_on = 0;
   std::memset(&L->diag, 0, sizeof(L->diag));
   L->timing_on = 0;
@@ -914,6 +984,7 @@ exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer) {
   if (layer->ev_made)
     for (int i = 0; i < 5; ++i) (void)hipEventDestroy(layer->ev[i]);
 
+  if (layer->scales) (void)hipFree(layer->scales);
   if (layer->sh_dense_t[0]) {
     hipError_t e = hipFree(layer->sh_dense_t[0]);
     if (e != hipSuccess) {

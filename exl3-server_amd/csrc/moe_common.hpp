@@ -61,6 +61,11 @@ struct MoeArgs {
   const float *router_bias;   // (E) f32
   const ExpertTab *tab;       // E (+1) entries
   const uint16_t *sh_dense[3];  // f16 shared expert weights, transposed (out, in), when dense
+  // suh/svh of every expert stacked by expert (entry E: a trellis shared expert):
+  // suh_s[0..1] (E + 1, H), svh_s[0..1] (E + 1, Imax), suh_s[2] (E + 1, Imax),
+  // svh_s[2] (E + 1, H); an expert's scale is one load away from its id
+  const uint16_t *suh_s[3];
+  const uint16_t *svh_s[3];
   // workspace
   float *logits;       // (N, E, 8): router logit k-split partials, or (N, E) plain logits
   float *weights;      // (N, topk)

@@ -393,7 +393,7 @@ __global__ __launch_bounds__(256) void k_moe_rotate(MoeArgs a, int n_slots) {
   const int64_t slot = gw >> 1;
   const int e = slot < a.P ? a.slot_e[slot] : a.E;
   const uint16_t *hrow = a.h + (int64_t)a.sorted_row[slot] * a.H + 2 * lane;
-  const uint16_t *suh = a.tab[e].suh[proj] + 2 * lane;
+  const uint16_t *suh = a.suh_s[proj] + (int64_t)e * a.H + 2 * lane;
   uint32_t *out = reinterpret_cast<uint32_t *>(a.xrot + (slot * 2 + proj) * a.H);
   for (int b0 = 0; b0 < nblk; b0 += kRotBatch) {
     uint32_t hx[kRotBatch], sx[kRotBatch];
@@ -454,8 +454,8 @@ __global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_m
     vu[q] = *reinterpret_cast<const float2 *>(pu + o);
   }
   const int e = shared_mode ? a.E : a.slot_e[slot];
-  const exl3m::ExpertTab &tb = a.tab[e];
-  const uint16_t *svg_p = tb.svh[0], *svu_p = tb.svh[1], *sud_p = tb.suh[2];
+  const int64_t so = (int64_t)e * a.Imax;
+  const uint16_t *svg_p = a.svh_s[0] + so, *svu_p = a.svh_s[1] + so, *sud_p = a.suh_s[2] + so;
   const uint32_t svg = *reinterpret_cast<const uint32_t *>(svg_p + c);
   const uint32_t svu = *reinterpret_cast<const uint32_t *>(svu_p + c);
   const uint32_t sud = *reinterpret_cast<const uint32_t *>(sud_p + c);

@@ -215,9 +215,10 @@ exl3_status exl3_trellis_linear_grouped(const exl3_trellis_desc *members, int32_
 /* Validates a layer (every expert of a projection class must share shape, K and
  * codebook; moe_prep_of, glm5_moe.cpp:430-486) and uploads its device-resident
  * expert table (pointer and scale tables, the G5MoePrep equivalent). Synchronous.
- * Trellis weights are referenced, not copied. An f16 shared expert is copied once,
- * transposed to (out, in) for the matrix cores (3 * hidden * SI f16 of device memory
- * owned by the layer), so its weights must hold their final values at this call. */
+ * Trellis words and the router are referenced, not copied. Copied into device memory
+ * the layer owns (so these must hold their final values at this call): every expert's
+ * suh/svh, stacked by expert like G5MoePrep (glm5_moe.cpp:430-486), and an f16 shared
+ * expert, transposed to (out, in) for the matrix cores (3 * hidden * SI f16). */
 exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_moe_config *cfg,
                                   exl3_moe_layer_t *out);
 exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer);
