@@ -62,6 +62,21 @@ WORKLOADS = {
 HOT_BIAS = 0.23  # bias tilt that sends about a quarter of the selections to 8 hot experts
 
 
+VALU_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_glm5_b8_valu.md")
+
+
+def profiled_valu_busy(kernel):
+    """VALU issue fraction of `kernel` from the committed rocprofv3 counter summary of
+    the B=8 decode workload (the expert kernels are bound by decode VALU, not HBM), or None."""
+    import re
+    try:
+        text = open(VALU_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(rf"^{kernel} VALU busy: ([0-9.]+)$", text, re.M)
+    return float(m.group(1)) if m else None
+
+
 def build_layers(n_layers, seed, device, kind="glm5"):
     import numpy as np  # noqa: F401
     from exl3_amd import synth
@@ -278,11 +293,13 @@ def main():
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic("k_moe_gate_up") if args.workload == "glm5_moe_decode_b8" else None,
                      "algorithmic_bytes_per_launch": round(gu_bytes),
-                     "avg_launch_ms": round(gu_ms, 5)},
+                     "avg_launch_ms": round(gu_ms, 5),
+                     "valu_busy_profiled": profiled_valu_busy("k_moe_gate_up") if args.workload == "glm5_moe_decode_b8" else None},
         "roofline_down": {"kernel": "k_moe_down", "achieved": round(dn_gbps, 1),
                           "frac": round(dn_gbps / HBM_PEAK_GBPS, 4),
                           "traffic": measured_traffic("k_moe_down") if args.workload == "glm5_moe_decode_b8" else None,
-                          "algorithmic_bytes_per_launch": round(dn_bytes), "avg_launch_ms": round(dn_ms, 5)},
+                          "algorithmic_bytes_per_launch": round(dn_bytes), "avg_launch_ms": round(dn_ms, 5),
+                          "valu_busy_profiled": profiled_valu_busy("k_moe_down") if args.workload == "glm5_moe_decode_b8" else None},
         "routed_trellis_GBps": round(routed_gbps, 1),
         "distinct_experts_per_step": round(distinct, 2),
         "stages_ms": {k: round(tm[k] / calls, 5) for k in ("router_ms", "gate_up_ms", "down_ms",
