@@ -747,7 +747,7 @@ exl3_status check_linear(const exl3_linear_desc &d, int in, int out, const char 
 // Routing (+ dispatch): one workgroup for up to kRouteOneWg rows (routing and dispatch
 // in one launch); above that the rows' routing spreads over workgroups of 16 rows and
 // the dispatch follows in a one-workgroup launch.
-constexpr int kRouteOneWg = 64;
+constexpr int kRouteOneWg = 16;
 
 void launch_route(const MoeArgs &a, float *w_out, int32_t *id_out, int do_dispatch, hipStream_t st) {
   with_route_chunks(a.E, [&](auto jn) {
