@@ -41,13 +41,13 @@ __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 
 // ---------------------------------------------------------------------------------
 // L1. Router logits: logits[t][e] = sum_k f32(h[t][k]) * f32(router_w[e][k])
-// (glm5_moe.cpp:127-128) on the matrix cores, one wave task per (16 experts, k split);
-// f16*f16 products are exact in f32. The router sums the split partials in order.
+// (glm5_moe.cpp:127-128) on the matrix cores, one workgroup per (16 rows, 16 experts,
+// k split), its 4 waves on quarters of the split; f16*f16 products are exact in f32.
+// The router sums the split partials in order.
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_moe_pre(MoeArgs a) {
-  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (task < dense_mfma_tasks(a.N, a.H, a.E))
-    dense_mfma<kLogitChunk>(a.h, a.N, a.H, a.router_w, a.E, a.logits, task);
+  __shared__ float red[4 * 64 * 4];
+  dense_mfma_wg4(a.h, a.N, a.H, a.router_w, a.E, a.logits, blockIdx.x, red);
 }
 
 // ---------------------------------------------------------------------------------
@@ -326,7 +326,16 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
   if (!(mode & 2)) return;
   __syncthreads();
   if (a.P <= 64) {
-    if (wave == 0) dispatch_small(a, s_small);
+    if (wave == 0) {
+      // a dispatch-only launch (mode 2) did not route here: its pairs' experts come from
+      // the routing launch's id_out, not from this workgroup's LDS
+      if (!(mode & 1)) {
+        if (lane < a.P) s_small[lane] = id_out[lane];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      }
+      dispatch_small(a, s_small);
+    }
     return;
   }
 
@@ -694,7 +703,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.swiglu_limit = L->cfg.swiglu_limit;
   a.shared_kind = L->shared;
   a.logit_splits = dense_mfma_splits(a.H);
-  a.n_logit_blocks = (int)((dense_mfma_tasks(N, a.H, a.E) + 3) / 4);
+  a.n_logit_blocks = (int)dense_mfma_tasks(N, a.H, a.E);  // one task per workgroup
   a.fold = N >= long_min_rows();  // long runs: kLongRows-row passes, slices folded
   a.pass_rows = (int)std::min<int64_t>(N, 16);
   a.h = h;

@@ -35,7 +35,6 @@ typedef _Float16 f16x8_ __attribute__((ext_vector_type(8)));
 typedef float f32x4_ __attribute__((ext_vector_type(4)));
 
 constexpr int kDenseSlots = 8;   // partial slots per output (splits <= 8)
-constexpr int kLogitChunk = 16;  // MFMA steps per load round of the router logits
 
 __host__ __device__ constexpr int dense_mfma_splits(int in) {
   return (in / 128) % 8 == 0 ? 8 : ((in / 128) % 4 == 0 ? 4 : ((in / 128) % 2 == 0 ? 2 : 1));
@@ -78,6 +77,59 @@ __device__ __forceinline__ void dense_mfma(const uint16_t *__restrict__ x, int64
   for (int i = 0; i < 4; ++i) {
     const int64_t rr = r0 + 4 * g + i;
     if (rr < rows && n < out) part[(rr * out + n) * kDenseSlots + sp] = D[i];
+  }
+}
+
+// The same task (and output layout) computed by the 4 waves of a workgroup: wave w
+// takes the w-th quarter of the split's MFMA steps, and the split partial is
+// ((q0 + q1) + q2) + q3 of the quarters' accumulators, summed by wave 0 through LDS
+// (red: 4 * 64 * 4 floats). Four times the memory parallelism of dense_mfma for
+// launches too small to fill the machine (the router logits at decode batch sizes).
+__device__ __forceinline__ void dense_mfma_wg4(const uint16_t *__restrict__ x, int64_t rows, int in,
+                                               const uint16_t *__restrict__ wt, int out,
+                                               float *__restrict__ part, int64_t task, float *red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int S = dense_mfma_splits(in), sk = in / S, nsteps = sk / 32, nq = nsteps / 4;
+  const int n_nb = (out + 15) / 16;
+  const int sp = (int)(task % S);
+  const int nb = (int)((task / S) % n_nb);
+  const int64_t r0 = 16 * (task / ((int64_t)S * n_nb));
+  const int n = nb * 16 + (lane & 15), g = lane >> 4;
+  const int nc = n < out ? n : out - 1;
+  const int k0 = sp * sk + wave * nq * 32 + 8 * g;
+  const int64_t row = r0 + (lane & 15);
+  const int64_t rc = row < rows ? row : rows - 1;
+  constexpr int kQ = 4;  // steps per load round
+  f32x4_ D = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+  for (int q0 = 0; q0 < nq; q0 += kQ) {
+    f16x8_ A[kQ], B[kQ];
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const int k = k0 + 32 * min(q0 + q, nq - 1);
+      B[q] = *reinterpret_cast<const f16x8_ *>(wt + (int64_t)nc * in + k);
+      A[q] = *reinterpret_cast<const f16x8_ *>(x + rc * in + k);
+    }
+#pragma unroll
+    for (int q = 0; q < kQ; ++q)
+      if (q0 + q < nq) D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[q], B[q], D, 0, 0, 0);
+  }
+  reinterpret_cast<f32x4_ *>(red)[wave * 64 + lane] = D;
+  __syncthreads();
+  if (wave == 0) {
+    const f32x4_ *rq = reinterpret_cast<const f32x4_ *>(red);
+    f32x4_ t = rq[lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const f32x4_ u = rq[w * 64 + lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] = t[i] + u[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t rr = r0 + 4 * g + i;
+      if (rr < rows && n < out) part[(rr * out + n) * kDenseSlots + sp] = t[i];
+    }
   }
 }
 
