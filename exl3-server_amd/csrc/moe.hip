@@ -109,6 +109,23 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
 
+// The run record of run `run_i`: expert e's pointers from the expert table.
+__device__ __forceinline__ void write_run_rec(const MoeArgs &a, int run_i, int e, int off, int len,
+                                              int row0, const ExpertTab &t) {
+  exl3m::RunRec r;
+  r.e = e;
+  r.off = off;
+  r.len = len;
+  r.row0 = row0;
+  r.p[0] = t.tr[0];
+  r.p[1] = t.suh[0];
+  r.p[2] = t.tr[1];
+  r.p[3] = t.suh[1];
+  r.p[4] = t.tr[2];
+  r.p[5] = nullptr;
+  a.run_rec[run_i] = r;
+}
+
 // The dispatch of P <= 64 pairs by one wave (lane i = pair i, its expert in ids[i]):
 // the same stable sort by expert, run table and pass table as the workgroup-wide
 // counting sort. The 64 keys (expert, pair index) are sorted across the lanes by a
@@ -127,6 +144,8 @@ __device__ __forceinline__ uint32_t bitonic_step(uint32_t key, int k) {
 __device__ __forceinline__ void dispatch_small(const MoeArgs &a, const int *ids) {
   const int lane = threadIdx.x & 63;
   const int P = a.P, K = a.topk;
+  // pair `lane`'s expert table entry, loaded while the keys are sorted
+  const ExpertTab tab_l = a.tab[lane < P ? ids[lane] : 0];
   uint32_t key = lane < P ? (((uint32_t)ids[lane] << 6) | (uint32_t)lane) : 0xFFFFFFFFu;
 #pragma unroll
   for (int k = 2; k <= 64; k <<= 1) {
@@ -157,10 +176,18 @@ __device__ __forceinline__ void dispatch_small(const MoeArgs &a, const int *ids)
   // passes of <= kLongRows rows: with P <= 64 only one run can need two
   const uint64_t big = __ballot(start && len > kLongRows);
   const int pass_i = run_i + (big && __builtin_ctzll(big) < lane ? 1 : 0);
+  // the expert table entry of this position's pair (loaded by lane `pair`)
+  ExpertTab tp;
+  for (int j = 0; j < 3; ++j) {
+    tp.tr[j] = (const uint32_t *)__shfl((long long)(uintptr_t)tab_l.tr[j], pair, 64);
+    tp.suh[j] = (const uint16_t *)__shfl((long long)(uintptr_t)tab_l.suh[j], pair, 64);
+    tp.svh[j] = nullptr;
+  }
   if (start) {
     a.run_expert[run_i] = se;
     a.run_off[run_i] = lane;
     a.run_len[run_i] = len;
+    write_run_rec(a, run_i, se, lane, len, pair / K, tp);
     for (int q = 0; q * kLongRows < len; ++q) {
       a.pass_expert[pass_i + q] = se;
       a.pass_off[pass_i + q] = lane + q * kLongRows;
@@ -341,6 +368,8 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
 
   // Stable counting sort of the P = N*K pairs by expert (pair order b*K + k), the
   // order of the reference's stable_sort (glm5_moe.cpp:191-200).
+  __shared__ int s_run_of[kMaxE], s_base[kMaxE];  // per expert: its run, its first slot
+  const ExpertTab tab_t = a.tab[threadIdx.x < E ? threadIdx.x : 0];  // loaded during the count
   int *cnt = reinterpret_cast<int *>(&s_buf[0][0]);  // [16][kMaxE]
   for (int i = threadIdx.x; i < 16 * kMaxE; i += 1024) cnt[i] = 0;
   __syncthreads();
@@ -401,7 +430,10 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       a.run_expert[run_i] = t;
       a.run_off[run_i] = base_e;
       a.run_len[run_i] = tot;
+      write_run_rec(a, run_i, t, base_e, tot, 0, tab_t);  // row0 set by the scatter below
     }
+    s_run_of[t] = run_i;
+    s_base[t] = base_e;
     for (int j = 0; j < npass; ++j) {
       a.pass_expert[pass_i + j] = t;
       a.pass_off[pass_i + j] = base_e + j * kLongRows;
@@ -429,6 +461,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       a.sorted_rank[pos] = p % K;
       a.slot_e[pos] = e;
       a.slot[p] = pos;
+      if (pos == s_base[e]) a.run_rec[s_run_of[e]].row0 = p / K;
     }
     __builtin_amdgcn_wave_barrier();
     if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
@@ -625,7 +658,7 @@ namespace {
 struct MoeLayout {
   size_t total;
   size_t logits, weights, ids, sorted_row, sorted_rank, slot_e, slot, run_expert, run_off, run_len,
-      n_runs, pass_expert, pass_off, pass_len, n_passes;
+      n_runs, run_rec, pass_expert, pass_off, pass_len, n_passes;
   size_t yhat_gu, act, yhat_dn, dsh_gu, dsh_act, dsh_dn, xrot;
   int P, R, Imax, S_dn, max_passes;
 };
@@ -667,6 +700,7 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.run_off = take(4 * (size_t)m.R);
   m.run_len = take(4 * (size_t)m.R);
   m.n_runs = take(4);
+  m.run_rec = take(sizeof(exl3m::RunRec) * (size_t)m.R);
   m.max_passes = m.R + (m.P + kLongRows - 1) / kLongRows;
   m.pass_expert = take(4 * (size_t)m.max_passes);
   m.pass_off = take(4 * (size_t)m.max_passes);
@@ -726,6 +760,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.run_off = (int32_t *)(ws + m.run_off);
   a.run_len = (int32_t *)(ws + m.run_len);
   a.n_runs = (int32_t *)(ws + m.n_runs);
+  a.run_rec = (exl3m::RunRec *)(ws + m.run_rec);
   a.pass_expert = (int32_t *)(ws + m.pass_expert);
   a.pass_off = (int32_t *)(ws + m.pass_off);
   a.pass_len = (int32_t *)(ws + m.pass_len);

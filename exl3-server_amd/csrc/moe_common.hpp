@@ -32,6 +32,15 @@ struct ExpertTab {
   const uint16_t *svh[3];
 };
 
+// One run of the dispatch as the short-run expert kernels read it, in one round of
+// loads: the expert, its slots and first token row, and its tensors' pointers
+// (p[2j] = trellis of projection j, p[2j + 1] = its suh, j = 0, 1; p[4] = the down
+// trellis). Written by the dispatch from the expert table.
+struct alignas(16) RunRec {
+  int32_t e, off, len, row0;
+  const void *p[6];
+};
+
 enum SharedKind { kSharedNone = 0, kSharedTrellis = 1, kSharedDense = 2 };
 
 // Everything a kernel of one layer call needs, passed by value.
@@ -76,6 +85,7 @@ struct MoeArgs {
   int32_t *slot;         // (P): pair b*topk + k -> slot
   int32_t *run_expert, *run_off, *run_len;  // (R)
   int32_t *n_runs;
+  RunRec *run_rec;       // (R) the runs with their pointers (short-run kernels)
   int32_t *pass_expert;  // (R + ceil(P / kLongRows)) runs cut into passes of <= kLongRows rows
   int32_t *pass_off;
   int32_t *pass_len;

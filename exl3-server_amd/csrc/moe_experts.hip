@@ -94,10 +94,28 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExp
   b /= n_cb;
   const int proj = b & 1, u = b >> 1;
   RunInfo ri;
-  if (!run_info(a, u, shared_mode, ri)) return;
-  const exl3m::ExpertTab &tb = a.tab[ri.e];
-  const uint32_t *base = tb.tr[proj];
-  const uint16_t *suh = tb.suh[proj];
+  int row0;
+  const uint32_t *base;
+  const uint16_t *suh;
+  if (shared_mode) {
+    if (u > 0) return;
+    ri = RunInfo{a.E, a.P, a.N};
+    row0 = 0;
+    base = a.tab[a.E].tr[proj];
+    suh = a.tab[a.E].suh[proj];
+  } else {
+    // the run count and the run's record in one round of loads (the exit test reads
+    // every loaded word, so none of the loads waits for it)
+    const int nruns = *a.n_runs;
+    const exl3m::RunRec *rr = a.run_rec + min(u, a.R - 1);
+    const int4 hd = *reinterpret_cast<const int4 *>(rr);
+    const ulonglong2 pp = *reinterpret_cast<const ulonglong2 *>(&rr->p[2 * proj]);
+    if (u >= nruns || hd.z <= 0 || pp.x == 0 || pp.y == 0) return;
+    ri = RunInfo{hd.x, hd.y, hd.z};
+    row0 = hd.w;
+    base = reinterpret_cast<const uint32_t *>(pp.x);
+    suh = reinterpret_cast<const uint16_t *>(pp.y);
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int slice_k = kStepTiles * ss * 16;  // k values per slice
   const int nblk = slice_k / 128;
@@ -113,7 +131,8 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExp
     S.start(base, k_tiles, out / 16, sl * kStepTiles * ss, cb * 4 + wave);
     for (int bi = wave; bi < nr * nblk; bi += kGuThreads / 64) {
       const int r = bi / nblk, blk = bi % nblk;
-      const int row = a.sorted_row[ri.off + p0 + r];
+      // shared slots hold the rows in order; a run's first row is in its record
+      const int row = shared_mode ? p0 + r : (p0 + r == 0 ? row0 : a.sorted_row[ri.off + p0 + r]);
       const int kc = k_base + blk * 128 + 2 * lane;
       const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
       const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
@@ -158,8 +177,20 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExp
   b /= n_sl;
   const int cb = b % n_cb, u = b / n_cb;
   RunInfo ri;
-  if (!run_info(a, u, shared_mode, ri)) return;
-  const exl3m::ExpertTab &tb = a.tab[ri.e];
+  const uint32_t *base;
+  if (shared_mode) {
+    if (u > 0) return;
+    ri = RunInfo{a.E, a.P, a.N};
+    base = a.tab[a.E].tr[2];
+  } else {
+    const int nruns = *a.n_runs;
+    const exl3m::RunRec *rr = a.run_rec + min(u, a.R - 1);
+    const int4 hd = *reinterpret_cast<const int4 *>(rr);
+    const uint64_t p4 = *reinterpret_cast<const uint64_t *>(&rr->p[4]);
+    if (u >= nruns || hd.z <= 0 || p4 == 0) return;
+    ri = RunInfo{hd.x, hd.y, hd.z};
+    base = reinterpret_cast<const uint32_t *>(p4);
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int slice_k = kStepTiles * ss * 16;
   const int xs_stride = slice_k / 2;  // words per staged row
@@ -169,7 +200,7 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExp
   SliceStream<K, PD> S;
   for (int p0 = 0; p0 < ri.len; p0 += a.pass_rows) {
     const int nr = min(a.pass_rows, ri.len - p0);
-    S.start(tb.tr[2], k_tiles, a.H / 16, sl * kStepTiles * ss, cb * 4 + wave);
+    S.start(base, k_tiles, a.H / 16, sl * kStepTiles * ss, cb * 4 + wave);
     const int q_row = xs_stride / 4;  // 16-byte chunks per staged row
     for (int i = threadIdx.x; i < nr * q_row; i += kDnThreads) {
       const int r = i / q_row, q = i % q_row;
