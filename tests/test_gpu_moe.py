@@ -317,3 +317,75 @@ def test_prefill_2048_config5(oracle, dev):
     print(f"\nprefill 2048: hot fraction {hot_frac:.3f}, runs {len(runs['run_len'])}, "
           f"max run {max(runs['run_len'])}, sampled max|err|/rms {rel:.3g}, cos {cos:.7f}, flips {flips}")
     d.close()
+
+
+@pytest.mark.parametrize("gu_K,gu_cb,dn_K,dn_cb", [(1, 0, 2, 1), (2, 2, 3, 0), (3, 1, 6, 2), (5, 0, 7, 1),
+                                                   (6, 2, 8, 0), (7, 1, 1, 2), (8, 0, 4, 1)])
+def test_layer_k_codebook_sweep(oracle, dev, gu_K, gu_cb, dn_K, dn_cb):
+    # every K and codebook through the MoE expert kernels (gate/up and down), with a
+    # trellis shared expert; B=5 (short runs) and B=70 (the long-run kernels)
+    cfg = synth.MoeConfig(hidden=256, inter=384, n_experts=12, top_k=3, routed_scaling_factor=1.5,
+                          shared_inter=256, gate_up_K=gu_K, gate_up_cb=gu_cb, down_K=dn_K,
+                          down_cb=dn_cb, shared_K=dn_K, shared_cb=gu_cb)
+    layer = synth.make_layer(cfg, 300 + gu_K)
+    d = DeviceMoeLayer(layer, dev)
+    oc = ocfg_of(oracle, cfg, True)
+    for B in (5, 70):
+        h = synth.activations(300 + gu_K, f"kcb.x.{B}", B, cfg.hidden)
+        x = to_dev(h, dev, B, 1, cfg.hidden)
+        y = d(x)
+        _, ids = d.route(x)
+        logits = oracle.router_logits(h, layer.router_w)
+        idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+        want = oracle.moe_layer_routed(oc, [l.oracle_dict() for l in layer.experts],
+                                       [l.oracle_dict() for l in layer.shared], h, idx, w)
+        check_out(y, want)
+        if B == 70:  # long-run path == decode path, bit for bit
+            yc = y.view(B, -1).cpu()
+            for r in (0, 33, 69):
+                assert torch.equal(d(x[r:r + 1].contiguous()).view(-1).cpu(), yc[r]), r
+    d.close()
+
+
+def test_layer_many_experts_grouped(oracle, dev):
+    # E = 1024 (the largest routing table), 8 groups keeping 4, top-16, f16 shared expert
+    cfg = synth.MoeConfig(hidden=256, inter=128, n_experts=1024, top_k=16, n_group=8, topk_group=4,
+                          routed_scaling_factor=2.0, shared_inter=128, gate_up_K=2, gate_up_cb=1,
+                          down_K=3, down_cb=1, shared_K=0)
+    layer = synth.make_layer(cfg, 1024)
+    d = DeviceMoeLayer(layer, dev)
+    oc = ocfg_of(oracle, cfg, True)
+    for B in (3, 20):  # 48 pairs: one-wave dispatch; 320 pairs: workgroup counting sort
+        h = synth.activations(1024, f"many.x.{B}", B, cfg.hidden)
+        x = to_dev(h, dev, B, 1, cfg.hidden)
+        d.diag_reset()
+        d.diag_enable()
+        y = d(x)
+        _, ids = d.route(x)
+        logits = oracle.router_logits(h, layer.router_w)
+        idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+        hist = {}
+        for r in oracle.moe_runs(idx)["run_len"].tolist():
+            hist[min(r, 64)] = hist.get(min(r, 64), 0) + 1
+        assert d.diag()["run_hist"] == hist
+        want = oracle.moe_layer_routed(oc, [l.oracle_dict() for l in layer.experts],
+                                       [l.oracle_dict() for l in layer.shared], h, idx, w)
+        check_out(y, want)
+    d.close()
+
+
+@pytest.mark.parametrize("B", [8, 9, 16, 17, 64, 65])
+def test_dispatch_boundaries_rows_invariance(dev, B):
+    # the dispatch and routing paths change at 64 pairs, 16 rows and 65 rows: every
+    # batch row equals the same row alone, bit for bit
+    cfg = synth.MoeConfig(hidden=128, inter=128, n_experts=20, top_k=8, routed_scaling_factor=1.0,
+                          gate_up_K=4, gate_up_cb=1, down_K=5, down_cb=1, shared_inter=0)
+    layer = synth.make_layer(cfg, 77)
+    d = DeviceMoeLayer(layer, dev)
+    h = synth.activations(77, f"bnd.{B}", B, 128)
+    x = to_dev(h, dev, B, 1, 128)
+    yb = d(x).view(B, -1).cpu()
+    assert torch.isfinite(yb.float()).all()
+    for r in sorted({0, B // 2, B - 1}):
+        assert torch.equal(d(x[r:r + 1].contiguous()).view(-1).cpu(), yb[r]), r
+    d.close()
