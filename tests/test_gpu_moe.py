@@ -389,3 +389,28 @@ def test_dispatch_boundaries_rows_invariance(dev, B):
     for r in sorted({0, B // 2, B - 1}):
         assert torch.equal(d(x[r:r + 1].contiguous()).view(-1).cpu(), yb[r]), r
     d.close()
+
+
+def test_layer_large_hidden_many_slices(oracle, dev):
+    # hidden 8192 (16 gate/up k slices, the activation kernel's long slice sum) and
+    # intermediate 2048 (4 down slices, the combine's long slice sum); short and long runs
+    cfg = synth.MoeConfig(hidden=8192, inter=2048, n_experts=6, top_k=2, routed_scaling_factor=1.0,
+                          gate_up_K=2, gate_up_cb=1, down_K=2, down_cb=2, shared_inter=0)
+    layer = synth.make_layer(cfg, 8192)
+    d = DeviceMoeLayer(layer, dev)
+    oc = ocfg_of(oracle, cfg, False)
+    for B in (3, 66):
+        h = synth.activations(8192, f"big.x.{B}", B, cfg.hidden)
+        x = to_dev(h, dev, B, 1, cfg.hidden)
+        y = d(x)
+        _, ids = d.route(x)
+        logits = oracle.router_logits(h, layer.router_w)
+        idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+        rows = list(range(B)) if B < 8 else [0, 31, 65]
+        want = oracle.moe_layer_routed(oc, [l.oracle_dict() for l in layer.experts], None, h[rows],
+                                       idx[rows], w[rows])
+        check_out(y.view(B, -1)[rows], want)
+        if B == 66:
+            yc = y.view(B, -1).cpu()
+            assert torch.equal(d(x[31:32].contiguous()).view(-1).cpu(), yc[31])
+    d.close()
