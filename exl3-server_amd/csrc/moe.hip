@@ -393,32 +393,44 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
   // block exclusive scans of tot, of (tot > 0) and of the run's pass count (passes of
   // at most kLongRows rows, the work units of the long-run expert kernels)
   const int npass = (tot + kLongRows - 1) / kLongRows;
-  int v = tot, f = tot > 0 ? 1 : 0, g = npass;
+  // runs that need several row passes of the short-run kernels go first in the run
+  // records, so that their longer workgroups start early instead of ending the launch
+  const int big = tot > a.pass_rows ? 1 : 0;
+  int v = tot, f = tot > 0 ? 1 : 0, g = npass, q = big;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int ov = __shfl_up(v, d, 64), of = __shfl_up(f, d, 64), og = __shfl_up(g, d, 64);
+    const int oq = __shfl_up(q, d, 64);
     if (lane >= d) {
       v += ov;
       f += of;
       g += og;
+      q += oq;
     }
   }
-  __shared__ int s_wv[16], s_wf[16], s_wg[16];
+  __shared__ int s_wv[16], s_wf[16], s_wg[16], s_wq[16];
   if (lane == 63) {
     s_wv[wave] = v;
     s_wf[wave] = f;
     s_wg[wave] = g;
+    s_wq[wave] = q;
   }
   __syncthreads();
-  int pv = 0, pf = 0, pg = 0;
-  for (int w = 0; w < wave; ++w) {
-    pv += s_wv[w];
-    pf += s_wf[w];
-    pg += s_wg[w];
+  int pv = 0, pf = 0, pg = 0, pq = 0, nbig = 0;
+  for (int w = 0; w < 16; ++w) {
+    if (w < wave) {
+      pv += s_wv[w];
+      pf += s_wf[w];
+      pg += s_wg[w];
+      pq += s_wq[w];
+    }
+    nbig += s_wq[w];
   }
   const int base_e = pv + v - tot;           // exclusive
   const int run_i = pf + f - (tot > 0 ? 1 : 0);
   const int pass_i = pg + g - npass;
+  const int big_i = pq + q - big;            // among the big runs
+  const int rec_i = big ? big_i : nbig + (run_i - big_i);  // big runs first, order kept
   if (t < E) {
     int run = base_e;
     for (int w = 0; w < 16; ++w) {
@@ -430,9 +442,9 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       a.run_expert[run_i] = t;
       a.run_off[run_i] = base_e;
       a.run_len[run_i] = tot;
-      write_run_rec(a, run_i, t, base_e, tot, 0, tab_t);  // row0 set by the scatter below
+      write_run_rec(a, rec_i, t, base_e, tot, 0, tab_t);  // row0 set by the scatter below
     }
-    s_run_of[t] = run_i;
+    s_run_of[t] = rec_i;
     s_base[t] = base_e;
     for (int j = 0; j < npass; ++j) {
       a.pass_expert[pass_i + j] = t;
