@@ -54,17 +54,16 @@ using namespace exl3h;
 
 namespace {
 
-// Workspace carve-up for the single/grouped linear: xhat f16 (n, rows, in) then the
-// slice partials f32 (n, n_slices, rows, out).
+// Workspace of the single/grouped linear: the slice partials (n, n_slices, rows, out) f32
+// (the input Hadamard happens inside the QMV kernel).
 struct LinearWs {
-  size_t xhat_off, part_off, total;
+  size_t part_off, total;
 };
 
 LinearWs linear_ws(int in, int out, int64_t rows, int n) {
   LinearWs w;
-  w.xhat_off = 0;
-  w.part_off = align_up((size_t)n * rows * in * 2, 256);
-  w.total = w.part_off + align_up((size_t)n * qmv_slices(in) * rows * out * 4, 256);
+  w.part_off = 0;
+  w.total = align_up((size_t)n * qmv_slices(in) * rows * out * 4, 256);
   return w;
 }
 
@@ -77,7 +76,8 @@ exl3_status check_ws(void *ws, size_t bytes, size_t need) {
   return EXL3_OK;
 }
 
-// xhat -> partials -> (raw f32 | f16 via the output Hadamard), n members of one shape.
+// x (or xhat) -> partials -> (raw f32 | f16 via the output Hadamard), n members of one
+// shape.
 exl3_status linear_core(const exl3_trellis_desc *members, int n, const uint16_t *x,
                         int64_t rows, bool x_shared, bool x_is_xhat, const uint16_t *suh_stack,
                         const uint16_t *svh_stack, float *y32, uint16_t *y16, void *ws,
@@ -87,7 +87,6 @@ exl3_status linear_core(const exl3_trellis_desc *members, int n, const uint16_t 
   const LinearWs lw = linear_ws(in, out, rows, n < PtrTable::kMax ? n : PtrTable::kMax);
   exl3_status rc = check_ws(ws, ws_bytes, lw.total);
   if (rc) return rc;
-  uint16_t *xhat = reinterpret_cast<uint16_t *>((char *)ws + lw.xhat_off);
   float *part = reinterpret_cast<float *>((char *)ws + lw.part_off);
   const int n_sl = qmv_slices(in);
   for (int c0 = 0; c0 < n; c0 += PtrTable::kMax) {
@@ -101,25 +100,9 @@ exl3_status linear_core(const exl3_trellis_desc *members, int n, const uint16_t 
                           : (const void *)members[c0 + i].svh;
     }
     const uint16_t *xc = x + (x_shared ? 0 : (int64_t)c0 * rows * in);
-    const uint16_t *xh = xc;
-    int64_t x_stride = x_shared ? 0 : rows * in;
-    if (!x_is_xhat) {
-      // One xhat block per member (each member has its own suh), member-major.
-      if (x_shared) {
-        for (int i = 0; i < cn; ++i) {
-          PtrTable one{};
-          one.p[0] = su.p[i];
-          rc = launch_hadamard(xc, nullptr, rows, in, one, rows, xhat + (int64_t)i * rows * in, st);
-          if (rc) return rc;
-        }
-      } else {
-        rc = launch_hadamard(xc, nullptr, rows * cn, in, su, rows, xhat, st);
-        if (rc) return rc;
-      }
-      xh = xhat;
-      x_stride = rows * in;
-    }
-    rc = launch_qmv(w0, tr, cn, xh, x_stride, rows, part, st);
+    const int64_t x_stride = x_shared ? 0 : rows * in;
+    // from x, the QMV kernel applies each member's input Hadamard while it stages rows
+    rc = launch_qmv(w0, tr, cn, xc, x_stride, rows, part, st, x_is_xhat ? nullptr : &su);
     if (rc) return rc;
     rc = launch_qmv_finalize(cn, n_sl, rows, out, part,
                              y32 ? y32 + (int64_t)c0 * rows * out : nullptr,

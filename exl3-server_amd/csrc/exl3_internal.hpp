@@ -60,10 +60,11 @@ exl3_status launch_hadamard(const uint16_t *x16, const float *x32, int64_t rows,
                             hipStream_t st);
 
 // xhat: (n, rows, in) f16 (member stride rows*in, or 0 when shared); part: f32
-// (n, n_slices, rows, out).
+// (n, n_slices, rows, out). With suh (member m's scales in suh->p[m]), xhat is the raw
+// x and the kernel applies the input Hadamard itself.
 exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, int n,
                        const uint16_t *xhat, int64_t x_member_stride, int64_t rows, float *part,
-                       hipStream_t st);
+                       hipStream_t st, const PtrTable *suh = nullptr);
 // Sums the slice partials in slice order into y32 (raw f32, (n, rows, out)) or, through
 // the output Hadamard with member m's svh.p[m], into y16 (n, rows, out).
 exl3_status launch_qmv_finalize(int n, int n_sl, int64_t rows, int out, const float *part,

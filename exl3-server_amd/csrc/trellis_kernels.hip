@@ -147,7 +147,8 @@ template <int K, int CB, int PD>
 __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_n, int in,
                                              int out, const uint16_t *__restrict__ xhat,
                                              int64_t x_member_stride, int64_t rows,
-                                             int pass_rows, float *__restrict__ part) {
+                                             int pass_rows, float *__restrict__ part,
+                                             exl3h::PtrTable suh, int rotate) {
   __shared__ uint32_t xs[kPassRows * kQmvSliceWords];
   __shared__ u32x4 slots[4 * kSlotChunks];
   const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
@@ -159,11 +160,39 @@ __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_
   const int member = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 
-  const uint16_t *xm = xhat + member * x_member_stride + r0 * in + sl * slice_k;
-  for (int i = threadIdx.x; i < nr * xs_stride; i += 256) {
-    const int r = i / xs_stride, w = i % xs_stride;
-    xs[r * xs_stride + (w & ~7) + xpos(w & 7)] =
-        reinterpret_cast<const uint32_t *>(xm + (int64_t)r * in)[w];
+  if (rotate) {
+    // x, not xhat: the input Hadamard of the slice's 128-blocks (member's suh), in the
+    // workgroup, kBatch blocks per wave at a time with every load issued first
+    constexpr int kBatch = 4;
+    const uint16_t *xr = xhat + member * x_member_stride + r0 * in + sl * slice_k + 2 * lane;
+    const uint16_t *su = (const uint16_t *)suh.p[member] + sl * slice_k + 2 * lane;
+    const int nblk = slice_k / 128, items = nr * nblk;
+    for (int b0 = wave; b0 < items; b0 += 4 * kBatch) {
+      uint32_t hx[kBatch], sx[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int bi = min(b0 + 4 * q, items - 1);
+        hx[q] = *reinterpret_cast<const uint32_t *>(xr + (int64_t)(bi / nblk) * in + (bi % nblk) * 128);
+        sx[q] = *reinterpret_cast<const uint32_t *>(su + (bi % nblk) * 128);
+      }
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int bi = b0 + 4 * q;
+        if (bi < items) {
+          float v0 = f16_to_f32((uint16_t)(hx[q] & 0xffffu)), v1 = f16_to_f32((uint16_t)(hx[q] >> 16));
+          wave_had_pre(v0, v1, f16_to_f32((uint16_t)(sx[q] & 0xffffu)), f16_to_f32((uint16_t)(sx[q] >> 16)));
+          stage_pair(xs + (bi / nblk) * xs_stride, bi % nblk, lane,
+                     (uint32_t)f32_to_f16(v0) | ((uint32_t)f32_to_f16(v1) << 16));
+        }
+      }
+    }
+  } else {
+    const uint16_t *xm = xhat + member * x_member_stride + r0 * in + sl * slice_k;
+    for (int i = threadIdx.x; i < nr * xs_stride; i += 256) {
+      const int r = i / xs_stride, w = i % xs_stride;
+      xs[r * xs_stride + (w & ~7) + xpos(w & 7)] =
+          reinterpret_cast<const uint32_t *>(xm + (int64_t)r * in)[w];
+    }
   }
   __syncthreads();
   f32x4 D0, D1;
@@ -263,29 +292,33 @@ exl3_status launch_hadamard(const uint16_t *x16, const float *x32, int64_t rows,
 
 template <int K, int CB, int PD>
 static void qmv_go(dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in, int out,
-                   const uint16_t *xhat, int64_t xs, int64_t rows, int pass_rows, float *part) {
-  k_qmv<K, CB, PD><<<grid, 256, 0, st>>>(tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part);
+                   const uint16_t *xhat, int64_t xs, int64_t rows, int pass_rows, float *part,
+                   const PtrTable *suh) {
+  k_qmv<K, CB, PD><<<grid, 256, 0, st>>>(tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part,
+                                         suh ? *suh : PtrTable{}, suh ? 1 : 0);
 }
 
 template <int K, int CB>
 static void qmv_pd(int pd, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in,
                    int out, const uint16_t *xhat, int64_t xs, int64_t rows, int pass_rows,
-                   float *part) {
-  if (pd == 1) return qmv_go<K, CB, 1>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part);
+                   float *part, const PtrTable *suh) {
+  if (pd == 1)
+    return qmv_go<K, CB, 1>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh);
   if constexpr (K <= 4) {
-    if (pd >= 4) return qmv_go<K, CB, 4>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part);
+    if (pd >= 4)
+      return qmv_go<K, CB, 4>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh);
   }
-  qmv_go<K, CB, 2>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part);
+  qmv_go<K, CB, 2>(grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh);
 }
 
 template <int K>
 static void qmv_cb(int cb, int pd, dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n,
                    int in, int out, const uint16_t *xhat, int64_t xs, int64_t rows, int pass_rows,
-                   float *part) {
+                   float *part, const PtrTable *suh) {
   switch (cb) {
-    case 0: qmv_pd<K, 0>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part); break;
-    case 1: qmv_pd<K, 1>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part); break;
-    default: qmv_pd<K, 2>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part); break;
+    case 0: qmv_pd<K, 0>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
+    case 1: qmv_pd<K, 1>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
+    default: qmv_pd<K, 2>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
   }
 }
 
@@ -300,7 +333,7 @@ int qmv_slices(int in) { return n_slices(in / 16); }
 
 exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, int n,
                        const uint16_t *xhat, int64_t x_member_stride, int64_t rows, float *part,
-                       hipStream_t st) {
+                       hipStream_t st, const PtrTable *suh) {
   const int in = shape.in_features, out = shape.out_features;
   const int k_tiles = in / 16;
   const int pr = qmv_pass_rows(rows);
@@ -311,7 +344,7 @@ exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, 
 #define EXL3_K(KK)                                                                        \
   case KK:                                                                                \
     qmv_cb<KK>(shape.codebook, pd, grid, st, trellis, tiles_n, in, out, xhat,             \
-               x_member_stride, rows, pr, part);                                          \
+               x_member_stride, rows, pr, part, suh);                                     \
     break;
     EXL3_K(1) EXL3_K(2) EXL3_K(3) EXL3_K(4) EXL3_K(5) EXL3_K(6) EXL3_K(7) EXL3_K(8)
 #undef EXL3_K

@@ -65,7 +65,7 @@ def test_path_info_and_workspace_query():
     ws1 = L.exl3_trellis_workspace_size(C.byref(d), 1, 1)
     ws8 = L.exl3_trellis_workspace_size(C.byref(d), 8, 3)
     assert 0 < ws1 < ws8
-    assert ws1 >= 4096 * 2 + 8 * 1024 * 4  # xhat + 8 slice planes
+    assert ws1 >= 8 * 1024 * 4  # 8 slice planes of f32 partials
 
 
 def test_workspace_too_small_is_reported_before_launch():
