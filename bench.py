@@ -58,15 +58,16 @@ WORKLOADS = {
     "glm5_moe_staged_b64": ("glm5", 64, "configs[3]: 48 identical rows + 16 independent rows"),
     "glm5_moe_prefill_2048": ("prefill", 2048, "configs[4]: 2048-token prefill, gate/up K4 3inst, "
                                                "down K5 mul1, shared K6 mcg, 8 hot experts"),
-    "trellis_linear": ("linear", 1, "configs[1]: one trellis linear at rows=1 (in 4096), K=1..8 mcg"),
+    "trellis_linear": ("linear", 1, "configs[1]: one trellis linear at rows=1 (in 4096), K=1..8 x 3 codebooks"),
 }
 
 
 def bench_linear(args):
     """exl3_trellis_linear at rows = 1: in 4096 x out 24576 (the reference's headline GEMV
-    shape, perf.md:75) at K=4 mcg is the line's value, plus a K=1..8 mcg sweep at 4096 x
-    4096. Each shape rotates over enough distinct copies (>= 512 MB) that
-    the MALL cannot serve them; the time is HIP events around the timed calls."""
+    shape, perf.md:75) at K=4 mcg is the line's value, plus the K=1..8 x {3inst, mcg, mul1}
+    sweep at 4096 x 4096. Each shape rotates over enough distinct copies
+    (>= 512 MB) that the MALL cannot serve them; the time is HIP events around the timed
+    calls."""
     import ctypes as C
     import numpy as np
     import torch
@@ -76,13 +77,13 @@ def bench_linear(args):
 
     dev = torch.device("cuda:0")
 
-    def run(in_f, out_f, K, steps, warmup):
+    def run(in_f, out_f, K, steps, warmup, cb=1):
         nbytes = in_f * out_f // 256 * 32 * K
         copies = max(2, -(-(512 << 20) // nbytes))
         su = f16_from_bits(synth.normal_f16(1, "lin.suh", (in_f,), 1.0, 0.05), dev)
         sv = f16_from_bits(synth.normal_f16(1, "lin.svh", (out_f,), 1.0, 0.05), dev)
         ws = [TrellisWeight(trellis_words_torch(args.seed, f"lin.{K}.{i}", in_f, out_f, K, dev), su, sv,
-                            in_f, out_f, K, 1) for i in range(copies)]
+                            in_f, out_f, K, cb) for i in range(copies)]
         x = torch.from_numpy(synth.activations(1, "lin.x", 1, in_f).view(np.float16)).to(dev)
         y = torch.empty((1, out_f), dtype=torch.float16, device=dev)
         d0 = ws[0].desc()
@@ -112,9 +113,10 @@ def bench_linear(args):
     warmup = args.warmup if args.warmup is not None else 40
     ms, gbps = run(4096, 24576, 4, steps, warmup)
     sweep = {}
-    for K in range(1, 9):
-        kms, kg = run(4096, 4096, K, steps, warmup)
-        sweep[f"K{K}"] = {"ms": round(kms, 5), "GBps": round(kg, 1)}
+    for cb, name in ((0, "3inst"), (1, "mcg"), (2, "mul1")):
+        for K in range(1, 9):
+            kms, kg = run(4096, 4096, K, steps, warmup, cb)
+            sweep[f"{name}_K{K}"] = {"ms": round(kms, 5), "GBps": round(kg, 1)}
     line = {
         "metric": "trellis linear GB/s on trellis bytes, rows=1, 1 MI355X", "value": round(gbps, 1),
         "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
@@ -122,10 +124,10 @@ def bench_linear(args):
         "data": "synthetic",
         "config": {"workload": "trellis_linear", "in": 4096, "out": 24576, "K": 4, "codebook": "mcg",
                    "rows": 1, "parallelism": "none (one GPU)"},
-        "roofline": {"kernel": "exl3_trellis_linear (pre-Hadamard, QMV, finalize)", "bound": "hbm",
+        "roofline": {"kernel": "exl3_trellis_linear (QMV with the input Hadamard, finalize)", "bound": "hbm",
                      "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
-        "sweep_4096x4096_mcg": sweep, "cpu_baseline": None,
+        "sweep_4096x4096": sweep, "cpu_baseline": None,
     }
     print(json.dumps(line))
 HOT_BIAS = 0.23  # bias tilt that sends about a quarter of the selections to 8 hot experts

@@ -9,14 +9,18 @@
 //                 per pass of up to 16 token rows of the run, the input Hadamard of the
 //                 slice's part of those rows into LDS, then one n-pair (32 columns) per
 //                 wave over the slice on the MFMA core -> raw f32 slice partials in
-//                 yhat_gu. Extra workgroups compute the f16 shared expert's down
-//                 partials.
-//  k_moe_down     workgroup = (run, 128-column block), 4 waves: prologue = gate/up slice
-//                 partials summed in slice order, their output Hadamards (svh), SwiGLU
-//                 with the swiglu_limit clamp (f16 op by op) and the down projection's
-//                 input Hadamard (suh), for the whole intermediate of each row; then the
-//                 down slices, the output Hadamard, and f16(f32(y) * w) per slot (or the
-//                 shared expert's output).
+//                 yhat_gu. Extra leading workgroups compute the f16 shared expert's
+//                 gate/up partials.
+//  k_moe_act      per (slot, 128-block): gate/up slice sums in order, output Hadamards
+//                 (svh), SwiGLU with the swiglu_limit clamp (f16 op by op) and the down
+//                 projection's input Hadamard (suh) -> act, in the MFMA k order.
+//  k_moe_down     workgroup = (run, 128-column block of H, k-slice of the intermediate),
+//                 4 waves, over act -> raw f32 slice partials in yhat_dn (the output
+//                 Hadamard and the routing weight are applied by k_moe_combine). Extra
+//                 leading workgroups compute the f16 shared expert's down partials.
+//  *_long         calls of many rows: 48-row passes, every k slice in one workgroup,
+//                 slice partials folded in registers; k_moe_rotate stages the rotated
+//                 gate/up inputs once per (slot, projection).
 //
 // Per token row and expert the arithmetic is exl3_trellis_linear's (same input
 // Hadamard, k slices and slice order, output Hadamard), and the MFMA rows of a pass
@@ -75,24 +79,22 @@ __device__ __forceinline__ bool run_info(const MoeArgs &a, int u, int shared_mod
 // Workgroup = (run, projection, 128-column block, k-slice of H); 4 waves, wave w owns
 // n-pair 4*cb + w. Per pass of up to 16 token rows of the run: the input Hadamard of
 // the slice's 128-blocks into LDS, then one slice per wave, raw f32 partials to yhat_gu
-// (summed in slice order by k_moe_act).
+// (summed in slice order by k_moe_act). Grid: x = k-slice, y = 128-column block,
+// z = dense_z planes of f16 shared-expert workgroups, then 2 * run + projection (a 3-D
+// grid, so that no wave spends VALU on dividing its block index).
 template <int K, int CB, int PD>
-__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExpertWaves<K>, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_blocks) {
+__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExpertWaves<K>, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_z) {
   extern __shared__ uint32_t smem[];
-  if ((int)blockIdx.x < dense_blocks) {
-    shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu, blockIdx.x,
-                         kGuThreads / 64);
+  if ((int)blockIdx.z < dense_z) {
+    shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu,
+                         (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x, kGuThreads / 64);
     return;
   }
   const int out = shared_mode ? a.SI : a.I;
-  const int n_cb = out / 128;
-  const int k_tiles = a.H / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
-  int b = blockIdx.x - dense_blocks;
-  const int sl = b % n_sl;
-  b /= n_sl;
-  const int cb = b % n_cb;
-  b /= n_cb;
-  const int proj = b & 1, u = b >> 1;
+  const int k_tiles = a.H / 16, ss = slice_steps(k_tiles), n_sl = gridDim.x;
+  const int sl = blockIdx.x, cb = blockIdx.y;
+  const int zz = blockIdx.z - dense_z;
+  const int proj = zz & 1, u = zz >> 1;
   RunInfo ri;
   int row0;
   const uint32_t *base;
@@ -118,7 +120,8 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExp
   }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int slice_k = kStepTiles * ss * 16;  // k values per slice
-  const int nblk = slice_k / 128;
+  const int nblk = slice_k / 128;           // a power of two (slice_steps)
+  const int nblk_lg = __builtin_ctz(nblk);
   const int xs_stride = slice_k / 2;         // words per staged row
   const int k_base = sl * slice_k;
   uint32_t *xs = smem;
@@ -130,7 +133,7 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExp
     // the slice's first ring words are in flight while the rows are staged
     S.start(base, k_tiles, out / 16, sl * kStepTiles * ss, cb * 4 + wave);
     for (int bi = wave; bi < nr * nblk; bi += kGuThreads / 64) {
-      const int r = bi / nblk, blk = bi % nblk;
+      const int r = bi >> nblk_lg, blk = bi & (nblk - 1);
       // shared slots hold the rows in order; a run's first row is in its record
       const int row = shared_mode ? p0 + r : (p0 + r == 0 ? row0 : a.sorted_row[ri.off + p0 + r]);
       const int kc = k_base + blk * 128 + 2 * lane;
@@ -161,21 +164,19 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExp
 // owns n-pair 4*cb + w. Per pass of up to 16 token rows: the rows' rotated SwiGLU
 // outputs (k_moe_act, already in the MFMA k order) for the slice into LDS, one slice
 // per wave, raw f32 partials to yhat_dn (the output Hadamard and the routing weight
-// are applied by k_moe_combine).
+// are applied by k_moe_combine). Grid: x = k-slice, y = 128-column block, z = dense_z
+// planes of f16 shared-expert workgroups, then the run.
 template <int K, int CB, int PD>
-__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExpertWaves<K>, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_blocks) {
+__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExpertWaves<K>, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_z) {
   extern __shared__ uint32_t smem[];
-  if ((int)blockIdx.x < dense_blocks) {
-    shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn, blockIdx.x, kDnThreads / 64);
+  if ((int)blockIdx.z < dense_z) {
+    shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn,
+                      (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x, kDnThreads / 64);
     return;
   }
   const int in = shared_mode ? a.SI : a.I;
-  const int n_cb = a.H / 128;
-  const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
-  int b = blockIdx.x - dense_blocks;
-  const int sl = b % n_sl;
-  b /= n_sl;
-  const int cb = b % n_cb, u = b / n_cb;
+  const int k_tiles = in / 16, ss = slice_steps(k_tiles);
+  const int sl = blockIdx.x, cb = blockIdx.y, u = blockIdx.z - dense_z;
   RunInfo ri;
   const uint32_t *base;
   if (shared_mode) {
@@ -201,9 +202,10 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExp
   for (int p0 = 0; p0 < ri.len; p0 += a.pass_rows) {
     const int nr = min(a.pass_rows, ri.len - p0);
     S.start(base, k_tiles, a.H / 16, sl * kStepTiles * ss, cb * 4 + wave);
-    const int q_row = xs_stride / 4;  // 16-byte chunks per staged row
+    const int q_row = xs_stride / 4;  // 16-byte chunks per staged row (a power of two)
+    const int q_lg = __builtin_ctz(q_row);
     for (int i = threadIdx.x; i < nr * q_row; i += kDnThreads) {
-      const int r = i / q_row, q = i % q_row;
+      const int r = i >> q_lg, q = i & (q_row - 1);
       reinterpret_cast<uint4 *>(xs + r * xs_stride)[q] = reinterpret_cast<const uint4 *>(
           a.act + (int64_t)(ri.off + p0 + r) * a.Imax + sl * slice_k)[q];
     }
@@ -530,7 +532,7 @@ int moe_slices(int in) { return n_slices(in / 16); }
 
 
 template <typename Kern>
-static exl3_status launch_kernel(Kern k, unsigned blocks, unsigned threads, size_t lds, hipStream_t st,
+static exl3_status launch_kernel(Kern k, dim3 blocks, unsigned threads, size_t lds, hipStream_t st,
                                  const MoeArgs &a, int shared_mode, int dense_blocks, bool &attr_set) {
   if (!attr_set) {
     // above the 64 KB default; leaves room for the kernels' static LDS
@@ -544,7 +546,7 @@ static exl3_status launch_kernel(Kern k, unsigned blocks, unsigned threads, size
 
 // which: 0 = gate/up, 1 = down.
 template <int K, int CB, int PD>
-static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
+static exl3_status moe_go(int which, dim3 blocks, hipStream_t st, const MoeArgs &a,
                           int shared_mode, int dense_blocks) {
   const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
   if (a.fold) {
@@ -570,7 +572,7 @@ static exl3_status moe_go(int which, unsigned blocks, hipStream_t st, const MoeA
 }
 
 template <int K, int CB>
-static exl3_status moe_pd(int pd, int which, unsigned blocks, hipStream_t st, const MoeArgs &a,
+static exl3_status moe_pd(int pd, int which, dim3 blocks, hipStream_t st, const MoeArgs &a,
                           int shared_mode, int dense_blocks) {
   if (pd == 1) return moe_go<K, CB, 1>(which, blocks, st, a, shared_mode, dense_blocks);
   if constexpr (K <= 4) {
@@ -594,7 +596,8 @@ static int moe_prefetch(int k_tiles, int K) {
 
 // which: 0 = gate/up, 1 = down, over `runs` runs (routed: the dispatch's run table,
 // bounded by R; shared_mode 1: the one trellis-shared run). dense: prepend the f16
-// shared expert's workgroups for this projection.
+// shared expert's workgroups for this projection (short-run kernels: whole z planes of
+// the 3-D grid, the workgroups past the shared expert's tasks return at once).
 exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeArgs &a,
                               int shared_mode, bool dense, hipStream_t st) {
   const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
@@ -612,17 +615,30 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
       !dense ? 0
              : (which == 0 ? shared_gate_up_blocks(a.N, a.H, a.SI, waves)
                            : shared_down_blocks(a.N, a.H, a.SI, waves));
-  blocks += dense_blocks;
-  if (blocks == 0) return EXL3_OK;
-  if (blocks > 0x7fffffff) return fail(EXL3_ERR_UNSUPPORTED, "expert launch too large");
+  dim3 ub;
+  int dense_arg = dense_blocks;
+  if (a.fold) {
+    blocks += dense_blocks;
+    if (blocks == 0) return EXL3_OK;
+    if (blocks > 0x7fffffff) return fail(EXL3_ERR_UNSUPPORTED, "expert launch too large");
+    ub = dim3((unsigned)blocks);
+  } else {
+    // x = k-slice, y = 128-column block, z = dense planes, then (run, projection)
+    const int plane = n_sl * (out / 128);
+    const int dense_z = (dense_blocks + plane - 1) / plane;
+    const int64_t z = runs * (which == 0 ? 2 : 1) + dense_z;
+    if (z == 0) return EXL3_OK;
+    if (z > 65535) return fail(EXL3_ERR_UNSUPPORTED, "expert launch too large");
+    ub = dim3((unsigned)n_sl, (unsigned)(out / 128), (unsigned)z);
+    dense_arg = dense_z;
+  }
   const int pd = a.fold ? std::min(moe_prefetch(in / 16, K), 2) : moe_prefetch(in / 16, K);
   exl3_status rc = EXL3_OK;
-  const unsigned ub = (unsigned)blocks;
 #define EXL3_KC(KK)                                                                            \
   case KK:                                                                                     \
-    if (cb == 0) rc = moe_pd<KK, 0>(pd, which, ub, st, a, shared_mode, dense_blocks);         \
-    else if (cb == 1) rc = moe_pd<KK, 1>(pd, which, ub, st, a, shared_mode, dense_blocks);    \
-    else rc = moe_pd<KK, 2>(pd, which, ub, st, a, shared_mode, dense_blocks);                 \
+    if (cb == 0) rc = moe_pd<KK, 0>(pd, which, ub, st, a, shared_mode, dense_arg);         \
+    else if (cb == 1) rc = moe_pd<KK, 1>(pd, which, ub, st, a, shared_mode, dense_arg);    \
+    else rc = moe_pd<KK, 2>(pd, which, ub, st, a, shared_mode, dense_arg);                 \
     break;
   switch (K) {
     EXL3_KC(1) EXL3_KC(2) EXL3_KC(3) EXL3_KC(4) EXL3_KC(5) EXL3_KC(6) EXL3_KC(7) EXL3_KC(8)

@@ -153,9 +153,11 @@ __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_
   __shared__ u32x4 slots[4 * kSlotChunks];
   const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
   const int slice_k = kStepTiles * ss * 16, xs_stride = slice_k / 2;
-  const int n_cb = out / 128;
-  const int cb = blockIdx.x % n_cb, sl = blockIdx.x / n_cb;
-  const int64_t r0 = (int64_t)blockIdx.y * pass_rows;
+  // grid: x = 128-column block, y = row block * n_sl + k-slice, z = member (one row
+  // block, the decode case, needs no division)
+  const int cb = blockIdx.x;
+  const int sl = (int)gridDim.y == n_sl ? (int)blockIdx.y : (int)blockIdx.y % n_sl;
+  const int64_t r0 = (int64_t)((int)gridDim.y == n_sl ? 0 : (int)blockIdx.y / n_sl) * pass_rows;
   const int nr = (int)min<int64_t>(pass_rows, rows - r0);
   const int member = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -166,14 +168,16 @@ __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_
     constexpr int kBatch = 4;
     const uint16_t *xr = xhat + member * x_member_stride + r0 * in + sl * slice_k + 2 * lane;
     const uint16_t *su = (const uint16_t *)suh.p[member] + sl * slice_k + 2 * lane;
-    const int nblk = slice_k / 128, items = nr * nblk;
+    // blocks per row: slice_k / 128 = ss / 2, a power of two
+    const int nblk = slice_k / 128, nblk_lg = __builtin_ctz(nblk), items = nr * nblk;
     for (int b0 = wave; b0 < items; b0 += 4 * kBatch) {
       uint32_t hx[kBatch], sx[kBatch];
 #pragma unroll
       for (int q = 0; q < kBatch; ++q) {
         const int bi = min(b0 + 4 * q, items - 1);
-        hx[q] = *reinterpret_cast<const uint32_t *>(xr + (int64_t)(bi / nblk) * in + (bi % nblk) * 128);
-        sx[q] = *reinterpret_cast<const uint32_t *>(su + (bi % nblk) * 128);
+        hx[q] = *reinterpret_cast<const uint32_t *>(xr + (int64_t)(bi >> nblk_lg) * in +
+                                                    (bi & (nblk - 1)) * 128);
+        sx[q] = *reinterpret_cast<const uint32_t *>(su + (bi & (nblk - 1)) * 128);
       }
 #pragma unroll
       for (int q = 0; q < kBatch; ++q) {
@@ -181,15 +185,16 @@ __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_
         if (bi < items) {
           float v0 = f16_to_f32((uint16_t)(hx[q] & 0xffffu)), v1 = f16_to_f32((uint16_t)(hx[q] >> 16));
           wave_had_pre(v0, v1, f16_to_f32((uint16_t)(sx[q] & 0xffffu)), f16_to_f32((uint16_t)(sx[q] >> 16)));
-          stage_pair(xs + (bi / nblk) * xs_stride, bi % nblk, lane,
+          stage_pair(xs + (bi >> nblk_lg) * xs_stride, bi & (nblk - 1), lane,
                      (uint32_t)f32_to_f16(v0) | ((uint32_t)f32_to_f16(v1) << 16));
         }
       }
     }
   } else {
     const uint16_t *xm = xhat + member * x_member_stride + r0 * in + sl * slice_k;
+    const int xs_lg = __builtin_ctz(xs_stride);  // xs_stride = 32 * ss, a power of two
     for (int i = threadIdx.x; i < nr * xs_stride; i += 256) {
-      const int r = i / xs_stride, w = i % xs_stride;
+      const int r = i >> xs_lg, w = i & (xs_stride - 1);
       xs[r * xs_stride + (w & ~7) + xpos(w & 7)] =
           reinterpret_cast<const uint32_t *>(xm + (int64_t)r * in)[w];
     }
@@ -227,10 +232,23 @@ __global__ __launch_bounds__(256) void k_qmv_finalize(int n, int n_sl, int64_t r
   const int member = (int)(rest / rows);
   const int c = cb * 128 + 2 * lane;
   const float *p = part + ((int64_t)member * n_sl * rows + row) * out + c;
-  float v0 = p[0], v1 = p[1];
-  for (int s = 1; s < n_sl; ++s) {
-    v0 += p[(int64_t)s * rows * out];
-    v1 += p[(int64_t)s * rows * out + 1];
+  // slice partials summed in slice order; the loads of 8 slices are issued together
+  float v0 = 0.0f, v1 = 0.0f;
+  for (int s0 = 0; s0 < n_sl; s0 += 8) {
+    float2 v[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      v[s] = *reinterpret_cast<const float2 *>(p + (int64_t)min(s0 + s, n_sl - 1) * rows * out);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s0 + s == 0) {
+        v0 = v[0].x;
+        v1 = v[0].y;
+      } else if (s0 + s < n_sl) {
+        v0 += v[s].x;
+        v1 += v[s].y;
+      }
+    }
   }
   const int64_t o = ((int64_t)member * rows + row) * out + c;
   if (y32) {
@@ -337,8 +355,9 @@ exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, 
   const int in = shape.in_features, out = shape.out_features;
   const int k_tiles = in / 16;
   const int pr = qmv_pass_rows(rows);
-  dim3 grid((unsigned)((out / 128) * n_slices(k_tiles)), (unsigned)((rows + pr - 1) / pr),
-            (unsigned)n);
+  const int64_t gy = (int64_t)n_slices(k_tiles) * ((rows + pr - 1) / pr);
+  if (gy > 65535 || n > 65535) return fail(EXL3_ERR_UNSUPPORTED, "linear launch too large");
+  dim3 grid((unsigned)(out / 128), (unsigned)gy, (unsigned)n);
   const int tiles_n = out / 16, pd = prefetch_steps(k_tiles, shape.K);
   switch (shape.K) {
 #define EXL3_K(KK)                                                                        \
