@@ -662,6 +662,11 @@ struct exl3_moe_layer_s {
   exl3_moe_timing timing;
   hipEvent_t ev[5];
   bool ev_made;
+  // calls of the long-run kernels with a trellis shared expert: the shared expert's
+  // launches go on a second stream, beside the routed ones, joined before the combine
+  hipStream_t side;
+  hipEvent_t fork, join;
+  bool side_made;
   std::mutex mu;
 };
 
@@ -1029,6 +1034,7 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
   L->diag_on = 0;
   std::memset(&L->diag, 0, sizeof(L->diag));
   L->timing_on = 0;
+  L->side_made = false;
   std::memset(&L->timing, 0, sizeof(L->timing));
   L->ev_made = false;
   *out = L;
@@ -1039,6 +1045,11 @@ exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer) {
   if (!layer) return EXL3_OK;
   if (layer->ev_made)
     for (int i = 0; i < 5; ++i) (void)hipEventDestroy(layer->ev[i]);
+  if (layer->side_made) {
+    (void)hipEventDestroy(layer->fork);
+    (void)hipEventDestroy(layer->join);
+    (void)hipStreamDestroy(layer->side);
+  }
 
   if (layer->scales) (void)hipFree(layer->scales);
   if (layer->sh_dense_t[0]) {
@@ -1106,6 +1117,29 @@ exl3_status exl3_moe_topk_route(const float *logits, const float *bias, int64_t 
   return EXL3_OK;
 }
 
+namespace {
+// EXL3_MOE_SIDE_STREAM=0 keeps the trellis shared expert on the caller's stream.
+bool side_stream_on() {
+  static const bool v = [] {
+    const char *e = std::getenv("EXL3_MOE_SIDE_STREAM");
+    return !(e && std::atoi(e) == 0);
+  }();
+  return v;
+}
+
+// The trellis shared expert: every token row through the expert kernels (one run of
+// the short-run kernels, or kLongRows-row passes of the long-run kernels).
+exl3_status launch_shared_trellis(const exl3_moe_layer_s *layer, const MoeArgs &a, int64_t N,
+                                  hipStream_t st) {
+  const int64_t sh_units = a.fold ? (N + kLongRows - 1) / kLongRows : 1;
+  exl3_status rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, sh_units, a, 1, false, st);
+  if (rc) return rc;
+  rc = launch_moe_act(a, 1, 0, st);
+  if (rc) return rc;
+  return launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, sh_units, a, 1, false, st);
+}
+}  // namespace
+
 exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B, int64_t Lq,
                            uint16_t *out, void *workspace, size_t workspace_bytes,
                            exl3_stream_t stream) {
@@ -1136,6 +1170,25 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
     rc = launch_moe_rotate(a, layer->shared == exl3m::kSharedTrellis, st);
     if (rc) return rc;
   }
+  // long-run calls: a trellis shared expert (under one wave of the machine on its own)
+  // runs on the layer's second stream while the routed experts run on the caller's
+  const bool side = a.fold && layer->shared == exl3m::kSharedTrellis && side_stream_on();
+  if (side) {
+    // one caller at a time records the fork and join (calls on other threads and
+    // streams would otherwise interleave them)
+    std::lock_guard<std::mutex> lk(layer->mu);
+    if (!layer->side_made) {
+      EXL3_HIP(hipStreamCreateWithFlags(&layer->side, hipStreamNonBlocking));
+      EXL3_HIP(hipEventCreateWithFlags(&layer->fork, hipEventDisableTiming));
+      EXL3_HIP(hipEventCreateWithFlags(&layer->join, hipEventDisableTiming));
+      layer->side_made = true;
+    }
+    EXL3_HIP(hipEventRecord(layer->fork, st));
+    EXL3_HIP(hipStreamWaitEvent(layer->side, layer->fork, 0));
+    rc = launch_shared_trellis(layer, a, N, layer->side);
+    if (rc) return rc;
+    EXL3_HIP(hipEventRecord(layer->join, layer->side));
+  }
   rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, units, a, 0, dense_sh, st);
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[2], st));
@@ -1147,13 +1200,10 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   if (rc) return rc;
   if (timed) EXL3_HIP(hipEventRecord(layer->ev[3], st));
   // a trellis shared expert: one run of every token row through the same kernels
-  if (layer->shared == exl3m::kSharedTrellis) {
-    const int64_t sh_units = a.fold ? (N + kLongRows - 1) / kLongRows : 1;
-    rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, sh_units, a, 1, false, st);
-    if (rc) return rc;
-    rc = launch_moe_act(a, 1, 0, st);
-    if (rc) return rc;
-    rc = launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, sh_units, a, 1, false, st);
+  if (side) {
+    EXL3_HIP(hipStreamWaitEvent(st, layer->join, 0));
+  } else if (layer->shared == exl3m::kSharedTrellis) {
+    rc = launch_shared_trellis(layer, a, N, st);
     if (rc) return rc;
   }
   // L6: combine
