@@ -182,17 +182,43 @@ __device__ __forceinline__ float xor_lanes(float v) {
 // ---------------------------------------------------------------------------------
 template <int D, int NB>
 __device__ __forceinline__ void fwht_stage(float (&v0)[NB], float (&v1)[NB]) {
-  float p0[NB], p1[NB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    p0[i] = xor_lanes<D>(v0[i]);
-    p1[i] = xor_lanes<D>(v1[i]);
-  }
   const bool upper = ((threadIdx.x & 63) & D) != 0;
+  if constexpr (NB == 1) {
+    // one vector: a select and an add per value (the per-stage sign register of the
+    // form below costs as much, and is kept live across callers' loops)
+    const float p0 = xor_lanes<D>(v0[0]), p1 = xor_lanes<D>(v1[0]);
+    v0[0] = upper ? (p0 - v0[0]) : (v0[0] + p0);
+    v1[0] = upper ? (p1 - v1[0]) : (v1[0] + p1);
+    return;
+  }
+  // upper lanes: p - v, lower lanes: v + p (p = v[lane ^ D]), as one fma(sgn, v, p) per
+  // value: sgn * v is exact, so the single rounding gives the same bits (signed zeros
+  // included) as the subtraction or addition, in one VALU op instead of a select and
+  // an add
+  const float sgn = upper ? -1.0f : 1.0f;
+  if constexpr (D == 32) {
+    // v_permlane32_swap(v, v) gives r0 = (lo: v[i], hi: v[i - 32]) and r1 = (lo:
+    // v[i + 32], hi: v[i]): lower lanes v + p = r0 + r1, upper lanes p - v = r0 - r1
 #pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    v0[i] = upper ? (p0[i] - v0[i]) : (v0[i] + p0[i]);
-    v1[i] = upper ? (p1[i] - v1[i]) : (v1[i] + p1[i]);
+    for (int i = 0; i < NB; ++i) {
+      const int a = __builtin_bit_cast(int, v0[i]), b = __builtin_bit_cast(int, v1[i]);
+      const auto ra = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+      const auto rb = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+      v0[i] = __builtin_fmaf(sgn, __builtin_bit_cast(float, (int)ra[1]), __builtin_bit_cast(float, (int)ra[0]));
+      v1[i] = __builtin_fmaf(sgn, __builtin_bit_cast(float, (int)rb[1]), __builtin_bit_cast(float, (int)rb[0]));
+    }
+  } else {
+    float p0[NB], p1[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      p0[i] = xor_lanes<D>(v0[i]);
+      p1[i] = xor_lanes<D>(v1[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      v0[i] = __builtin_fmaf(sgn, v0[i], p0[i]);
+      v1[i] = __builtin_fmaf(sgn, v1[i], p1[i]);
+    }
   }
 }
 
