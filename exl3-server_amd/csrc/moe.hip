@@ -50,6 +50,85 @@ __global__ __launch_bounds__(256) void k_moe_pre(MoeArgs a) {
   dense_mfma_wg4(a.h, a.N, a.H, a.router_w, a.E, a.logits, blockIdx.x, red);
 }
 
+// The same logits for calls of many rows, tiled: a workgroup computes a 64-row x
+// 64-expert tile of one k split, staging both operands through LDS 128 k at a time, so
+// each h row and router row is read once per tile instead of once per 16 x 16 task.
+// Per output the arithmetic is k_moe_pre's: the split's four quarters each accumulated
+// from zero by 16x16x32 MFMAs in step order, then ((q0 + q1) + q2) + q3, so the logits
+// (and the routing) are bit-identical whichever kernel ran. Grid: x = split, y =
+// expert block, z = row block; wave w owns rows 32(w & 1) .. +32 and experts
+// 32(w >> 1) .. +32 of the tile (2 x 2 MFMA tiles).
+constexpr int kPreTile = 64;
+constexpr int kPreChunk = 128;  // k per staging round
+constexpr int kPreStride = kPreChunk + 8;  // halves per staged row (16-byte pad)
+constexpr int kPreTiledMinRows = 256;
+
+__global__ __launch_bounds__(256) void k_moe_pre_tiled(MoeArgs a) {
+  __shared__ __align__(16) uint16_t sA[kPreTile * kPreStride];
+  __shared__ __align__(16) uint16_t sB[kPreTile * kPreStride];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+  const int H = a.H, E = a.E;
+  const int S = dense_mfma_splits(H), sk = H / S, qk = sk / 4;  // k per quarter
+  const int sp = blockIdx.x;
+  const int e0 = blockIdx.y * kPreTile;
+  const int64_t r0 = (int64_t)blockIdx.z * kPreTile;
+  const int wr = (wave & 1) * 32, we = (wave >> 1) * 32;
+  f32x4_ acc[2][2], D[2][2];
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) D[i][j] = f32x4_{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = 0; c0 < qk; c0 += kPreChunk) {
+      const int ck = min(kPreChunk, qk - c0);  // a multiple of 32
+      const int kk = sp * sk + q * qk + c0;
+      const int cpr = ck / 8;                  // 16-byte chunks per staged row
+      // rows and experts past the end load the last valid one (never stored)
+      for (int c = threadIdx.x; c < kPreTile * cpr; c += 256) {
+        const int r = c / cpr, kc = (c % cpr) * 8;
+        const int64_t row = min<int64_t>(r0 + r, a.N - 1);
+        const int e = min(e0 + r, E - 1);
+        *reinterpret_cast<uint4 *>(sA + r * kPreStride + kc) =
+            *reinterpret_cast<const uint4 *>(a.h + row * H + kk + kc);
+        *reinterpret_cast<uint4 *>(sB + r * kPreStride + kc) =
+            *reinterpret_cast<const uint4 *>(a.router_w + (int64_t)e * H + kk + kc);
+      }
+      __syncthreads();
+      for (int st = 0; st < ck / 32; ++st) {
+        const int ko = st * 32 + 8 * g;
+        f16x8_ A[2], B[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          A[i] = *reinterpret_cast<const f16x8_ *>(sA + (wr + 16 * i + (lane & 15)) * kPreStride + ko);
+          B[i] = *reinterpret_cast<const f16x8_ *>(sB + (we + 16 * i + (lane & 15)) * kPreStride + ko);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) D[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], D[i][j], 0, 0, 0);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[i][j][t] = q == 0 ? D[i][j][t] : acc[i][j][t] + D[i][j][t];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = e0 + we + 16 * j + (lane & 15);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int64_t row = r0 + wr + 16 * i + 4 * g + t;
+        if (row < a.N && e < E) a.logits[(row * E + e) * kDenseSlots + sp] = acc[i][j][t];
+      }
+    }
+}
+
 // ---------------------------------------------------------------------------------
 // Routing + dispatch, one workgroup of 16 waves (glm5_moe.cpp:16-60, 158-255).
 // ---------------------------------------------------------------------------------
@@ -827,8 +906,15 @@ void launch_route(const MoeArgs &a, float *w_out, int32_t *id_out, int do_dispat
 exl3_status launch_logits_route(exl3_moe_layer_s *L, const MoeArgs &a, float *w_out, int32_t *id_out,
                                 int do_dispatch, hipStream_t st) {
   (void)L;
-  k_moe_pre<<<a.n_logit_blocks, 256, 0, st>>>(a);
-  EXL3_LAUNCHED("k_moe_pre");
+  if (a.N >= kPreTiledMinRows && (a.N + kPreTile - 1) / kPreTile <= 65535) {
+    const dim3 grid((unsigned)dense_mfma_splits(a.H), (unsigned)((a.E + kPreTile - 1) / kPreTile),
+                    (unsigned)((a.N + kPreTile - 1) / kPreTile));
+    k_moe_pre_tiled<<<grid, 256, 0, st>>>(a);
+    EXL3_LAUNCHED("k_moe_pre_tiled");
+  } else {
+    k_moe_pre<<<a.n_logit_blocks, 256, 0, st>>>(a);
+    EXL3_LAUNCHED("k_moe_pre");
+  }
   launch_route(a, w_out, id_out, do_dispatch, st);
   EXL3_LAUNCHED("k_moe_route");
   return EXL3_OK;
