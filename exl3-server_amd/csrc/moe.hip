@@ -771,6 +771,19 @@ int64_t long_min_rows() {
   return v;
 }
 
+// Short-run calls of at least this many token rows rotate each (slot, projection)'s
+// input once (k_moe_rotate) and the gate/up workgroups copy it, instead of every
+// column block rotating its rows again: EXL3_MOE_XROT_ROWS, read once, default 32 (at
+// 64 rows 0.290 -> 0.275 ms; at 8 rows the extra launch costs more than it saves).
+int64_t xrot_min_rows() {
+  static const int64_t v = [] {
+    const char *e = std::getenv("EXL3_MOE_XROT_ROWS");
+    const long long x = e ? std::atoll(e) : 0;
+    return x > 0 ? (int64_t)x : (int64_t)32;
+  }();
+  return v;
+}
+
 MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   MoeLayout m{};
   const int H = L->H, I = L->I, E = L->E, K = L->topk, SI = L->shared ? L->SI : 0;
@@ -809,7 +822,7 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.dsh_gu = take(dense ? 4 * (size_t)2 * N * SI * kDenseSlots : 0);
   m.dsh_act = take(dense ? 2 * (size_t)N * SI : 0);
   m.dsh_dn = take(dense ? 4 * (size_t)N * H * kDenseSlots : 0);
-  m.xrot = take(N >= long_min_rows() ? 2 * (size_t)slots * 2 * H : 0);
+  m.xrot = take(N >= long_min_rows() || N >= xrot_min_rows() ? 2 * (size_t)slots * 2 * H : 0);
   m.total = o;
   return m;
 }
@@ -836,6 +849,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.n_logit_blocks = (int)dense_mfma_tasks(N, a.H, a.E);  // one task per workgroup
   a.fold = N >= long_min_rows();  // long runs: kLongRows-row passes, slices folded
   a.pass_rows = (int)std::min<int64_t>(N, 16);
+  a.xrot_rows = !a.fold && N >= xrot_min_rows();
   a.h = h;
   a.router_w = L->router_w;
   a.router_bias = L->router_bias;
@@ -1252,7 +1266,7 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   // L3: routed gate/up (+ the f16 shared expert's gate/up partials)
   const bool dense_sh = layer->shared == exl3m::kSharedDense;
   const int64_t units = a.fold ? m.max_passes : m.R;  // work units: runs or long-run passes
-  if (a.fold) {
+  if (a.fold || a.xrot_rows) {
     rc = launch_moe_rotate(a, layer->shared == exl3m::kSharedTrellis, st);
     if (rc) return rc;
   }

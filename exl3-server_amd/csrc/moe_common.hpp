@@ -64,6 +64,7 @@ struct MoeArgs {
   int logit_splits;   // k-split partials per logit (0: plain logits given by the caller)
   int fold;           // 1: expert kernels fold their k slices (one partial per output)
   int pass_rows;      // token rows per MFMA pass of the expert kernels (<= 16)
+  int xrot_rows;      // 1: the short-run gate/up kernel copies the rows k_moe_rotate rotated
   // inputs
   const uint16_t *h;          // (N, H) f16
   const uint16_t *router_w;   // (E, H) f16
@@ -93,7 +94,8 @@ struct MoeArgs {
   float *yhat_gu;      // (P + N, 2, S, Imax): gate/up k-slice partials (S slices of H)
                        // before the output Hadamard
   uint16_t *act;       // (P + N, Imax): rotated SwiGLU output per slot, MFMA k order
-  uint16_t *xrot;      // long-run mode: (P + N, 2, H) f16 rotated gate/up inputs, staged order
+  uint16_t *xrot;      // long-run mode or xrot_rows: (P + N, 2, H) f16 rotated gate/up
+                       // inputs, staged order
   int S_dn;            // slot stride of yhat_dn in slices: max(slices(I), slices(SI))
   float *yhat_dn;      // (P + N, S_dn, H): down k-slice partials per slot, before the
                        // output Hadamard (slots P.. = a trellis shared expert)

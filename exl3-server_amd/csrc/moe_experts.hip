@@ -132,16 +132,27 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExp
     const int nr = min(a.pass_rows, ri.len - p0);
     // the slice's first ring words are in flight while the rows are staged
     S.start(base, k_tiles, out / 16, sl * kStepTiles * ss, cb * 4 + wave);
-    for (int bi = wave; bi < nr * nblk; bi += kGuThreads / 64) {
-      const int r = bi >> nblk_lg, blk = bi & (nblk - 1);
-      // shared slots hold the rows in order; a run's first row is in its record
-      const int row = shared_mode ? p0 + r : (p0 + r == 0 ? row0 : a.sorted_row[ri.off + p0 + r]);
-      const int kc = k_base + blk * 128 + 2 * lane;
-      const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
-      const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
-      float v0 = lo16(hx), v1 = hi16(hx);
-      wave_had_pre(v0, v1, lo16(sx), hi16(sx));
-      stage_pair(xs + r * xs_stride, blk, lane, pack16(v0, v1));
+    if (a.xrot_rows) {
+      // rows already rotated by k_moe_rotate (x_rot of this projection, staged k
+      // order): 16-byte copies of the slice
+      const int q_row = xs_stride / 4, q_lg = __builtin_ctz(q_row);
+      for (int i = threadIdx.x; i < nr * q_row; i += kGuThreads) {
+        const int r = i >> q_lg, q = i & (q_row - 1);
+        reinterpret_cast<uint4 *>(xs + r * xs_stride)[q] = reinterpret_cast<const uint4 *>(
+            a.xrot + ((int64_t)(ri.off + p0 + r) * 2 + proj) * a.H + k_base)[q];
+      }
+    } else {
+      for (int bi = wave; bi < nr * nblk; bi += kGuThreads / 64) {
+        const int r = bi >> nblk_lg, blk = bi & (nblk - 1);
+        // shared slots hold the rows in order; a run's first row is in its record
+        const int row = shared_mode ? p0 + r : (p0 + r == 0 ? row0 : a.sorted_row[ri.off + p0 + r]);
+        const int kc = k_base + blk * 128 + 2 * lane;
+        const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
+        const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
+        float v0 = lo16(hx), v1 = hi16(hx);
+        wave_had_pre(v0, v1, lo16(sx), hi16(sx));
+        stage_pair(xs + r * xs_stride, blk, lane, pack16(v0, v1));
+      }
     }
     __syncthreads();
     f32x4 D0, D1;
