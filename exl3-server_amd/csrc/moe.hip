@@ -1134,9 +1134,27 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
   L->diag_on = 0;
   std::memset(&L->diag, 0, sizeof(L->diag));
   L->timing_on = 0;
-  L->side_made = false;
   std::memset(&L->timing, 0, sizeof(L->timing));
   L->ev_made = false;
+  L->side_made = false;
+  if (L->shared == exl3m::kSharedTrellis) {
+    // the second stream of long-run calls, made here so that no call creates it (a
+    // call may be under graph capture)
+    hipError_t e3 = hipStreamCreateWithFlags(&L->side, hipStreamNonBlocking);
+    if (e3 == hipSuccess) {
+      e3 = hipEventCreateWithFlags(&L->fork, hipEventDisableTiming);
+      if (e3 == hipSuccess) {
+        e3 = hipEventCreateWithFlags(&L->join, hipEventDisableTiming);
+        if (e3 == hipSuccess) L->side_made = true;
+        else (void)hipEventDestroy(L->fork);
+      }
+      if (!L->side_made) (void)hipStreamDestroy(L->side);
+    }
+    if (!L->side_made) {
+      (void)exl3_moe_layer_destroy(L);
+      return hip_check(e3, "layer stream");
+    }
+  }
   *out = L;
   return EXL3_OK;
 }
@@ -1272,17 +1290,11 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   }
   // long-run calls: a trellis shared expert (under one wave of the machine on its own)
   // runs on the layer's second stream while the routed experts run on the caller's
-  const bool side = a.fold && layer->shared == exl3m::kSharedTrellis && side_stream_on();
+  const bool side = a.fold && layer->side_made && side_stream_on();
   if (side) {
     // one caller at a time records the fork and join (calls on other threads and
     // streams would otherwise interleave them)
     std::lock_guard<std::mutex> lk(layer->mu);
-    if (!layer->side_made) {
-      EXL3_HIP(hipStreamCreateWithFlags(&layer->side, hipStreamNonBlocking));
-      EXL3_HIP(hipEventCreateWithFlags(&layer->fork, hipEventDisableTiming));
-      EXL3_HIP(hipEventCreateWithFlags(&layer->join, hipEventDisableTiming));
-      layer->side_made = true;
-    }
     EXL3_HIP(hipEventRecord(layer->fork, st));
     EXL3_HIP(hipStreamWaitEvent(layer->side, layer->fork, 0));
     rc = launch_shared_trellis(layer, a, N, layer->side);
