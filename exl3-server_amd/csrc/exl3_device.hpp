@@ -6,13 +6,10 @@
 // 32 "reference lanes") maps to tile element row = 2*(L%4) + {0,1,8,9}[i%4],
 // col = L/4 + 8*(i/4).
 //
-// Lane mapping used by every GEMV here (wave64): a wave works on 8 tiles that are
-// adjacent along n (128 output columns, one Hadamard block) at one k-tile. Eight
-// lanes share a tile; lane m of a tile holds that tile's ring words [m*K, m*K+K) plus
-// the word just before them, which is exactly the bit range of reference lanes
-// 4m..4m+3, i.e. all 16 k-rows of output columns m and m+8. A lane therefore finishes
-// whole dot products over the tile's 16 k values and needs no cross-lane reduction
-// inside a tile.
+// In the GEMV kernels eight lanes share a tile: lane m of a tile holds that tile's ring
+// words [m*K, m*K+K) plus the word just before them, which is exactly the bit range
+// of reference lanes 4m..4m+3, i.e. all 16 k-rows of output columns m and m+8 (the
+// wave-step layout over tiles is in qmv_core.hpp).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -68,25 +65,6 @@ __device__ __forceinline__ f16 decode_one(uint32_t s) {
   }
 }
 
-// Two states -> packed (w0, w1), ready for v_dot2_f32_f16.
-template <int CB>
-__device__ __forceinline__ f16x2 decode_pair(uint32_t s0, uint32_t s1) {
-  if constexpr (CB == 2) {
-    const uint32_t a0 = __builtin_amdgcn_sad_u8(s0 * 0x83DCD12Du, 0u, 0x6400u);
-    const uint32_t a1 = __builtin_amdgcn_sad_u8(s1 * 0x83DCD12Du, 0u, 0x6400u);
-    const f16x2 v = bitcast<f16x2>(a0 | (a1 << 16));
-    const f16x2 inv = {bitcast<f16>((uint16_t)0x1EEE), bitcast<f16>((uint16_t)0x1EEE)};
-    const f16x2 bias = {bitcast<f16>((uint16_t)0xC931), bitcast<f16>((uint16_t)0xC931)};
-    return __builtin_elementwise_fma(v, inv, bias);
-  } else {
-    const uint32_t m0 = (cb_hash<CB>(s0) & 0x8FFF8FFFu) ^ 0x3B603B60u;
-    const uint32_t m1 = (cb_hash<CB>(s1) & 0x8FFF8FFFu) ^ 0x3B603B60u;
-    const uint32_t lo = __builtin_amdgcn_perm(m1, m0, 0x05040100u);  // (m0.lo, m1.lo)
-    const uint32_t hi = __builtin_amdgcn_perm(m1, m0, 0x07060302u);  // (m0.hi, m1.hi)
-    return bitcast<f16x2>(lo) + bitcast<f16x2>(hi);
-  }
-}
-
 // ---------------------------------------------------------------------------------
 // Ring windows inside one lane's bit string. W[0] is the word before the lane's own
 // words, W[1..K] are its own K words (ring words m*K .. m*K+K-1 of the tile). The lane
@@ -111,45 +89,6 @@ __device__ __forceinline__ void lane_funnels(const uint32_t (&W)[K + 1], uint32_
   for (int w = 1; w <= K; ++w) F[w] = __builtin_amdgcn_alignbit(W[w - 1], W[w], 16);
 }
 
-// Loads this lane's K words and the preceding ring word of its tile. `tile` is the
-// tile's first word, m the lane's index inside the tile's 8 lanes.
-template <int K>
-__device__ __forceinline__ void lane_load(const uint32_t *__restrict__ tile, int m,
-                                          uint32_t (&W)[K + 1]) {
-  const uint32_t *p = tile + m * K;
-#pragma unroll
-  for (int w = 0; w < K; ++w) W[w + 1] = __builtin_nontemporal_load(p + w);
-  W[0] = __builtin_nontemporal_load(tile + ((m * K + 8 * K - 1) % (8 * K)));
-}
-
-// The 32 weights of one lane of one tile, multiplied into MB rows of x.
-// X[r] points at the tile's 16 x values of row r as 8 packed f16 pairs (k = 2u, 2u+1).
-// acc[r][0] accumulates output column m, acc[r][1] column m + 8 (m = lane's slot).
-// Position t = 8j + 4h + q covers k-row 2j + {0,1,8,9}[q] of column m + 8h, so
-// (q = 0,1) pairs with x pair j and (q = 2,3) with x pair 4 + j.
-template <int K, int CB, int MB>
-__device__ __forceinline__ void lane_tile_fma(const uint32_t (&W)[K + 1],
-                                              const uint32_t (&X)[MB][8],
-                                              float (&acc)[MB][2]) {
-  uint32_t F[K + 1];
-  lane_funnels<K>(W, F);
-#define EXL3_TILE_STEP(J, H)                                                             \
-  {                                                                                      \
-    const f16x2 wa = decode_pair<CB>(lane_state<K, 8 * J + 4 * H + 0>(W, F),           \
-                                     lane_state<K, 8 * J + 4 * H + 1>(W, F));           \
-    const f16x2 wb = decode_pair<CB>(lane_state<K, 8 * J + 4 * H + 2>(W, F),           \
-                                     lane_state<K, 8 * J + 4 * H + 3>(W, F));           \
-    _Pragma("unroll") for (int r = 0; r < MB; ++r) {                                     \
-      acc[r][H] = __builtin_amdgcn_fdot2(wa, bitcast<f16x2>(X[r][J]), acc[r][H], false); \
-      acc[r][H] = __builtin_amdgcn_fdot2(wb, bitcast<f16x2>(X[r][4 + J]), acc[r][H], false); \
-    }                                                                                    \
-  }
-  EXL3_TILE_STEP(0, 0) EXL3_TILE_STEP(0, 1)
-  EXL3_TILE_STEP(1, 0) EXL3_TILE_STEP(1, 1)
-  EXL3_TILE_STEP(2, 0) EXL3_TILE_STEP(2, 1)
-  EXL3_TILE_STEP(3, 0) EXL3_TILE_STEP(3, 1)
-#undef EXL3_TILE_STEP
-}
 
 // ---------------------------------------------------------------------------------
 // Lane exchange v <- v[lane ^ D] without the LDS crossbar's address arithmetic:

@@ -61,21 +61,6 @@ struct RunInfo {
   int e, off, len;
 };
 
-__device__ __forceinline__ bool run_info(const MoeArgs &a, int u, int shared_mode, RunInfo &ri) {
-  if (shared_mode) {
-    if (u > 0) return false;
-    ri.e = a.E;
-    ri.off = a.P;
-    ri.len = a.N;
-    return true;
-  }
-  if (u >= *a.n_runs) return false;
-  ri.e = a.run_expert[u];
-  ri.off = a.run_off[u];
-  ri.len = a.run_len[u];
-  return true;
-}
-
 // Workgroup = (run, projection, 128-column block, k-slice of H); 4 waves, wave w owns
 // n-pair 4*cb + w. Per pass of up to 16 token rows of the run: the input Hadamard of
 // the slice's 128-blocks into LDS, then one slice per wave, raw f32 partials to yhat_gu
