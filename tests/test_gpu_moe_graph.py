@@ -1,11 +1,14 @@
-"""The layer call captured into a HIP graph replays to the eager call's bytes.
+"""The layer call under graph capture and from several host threads.
+
+Captured into a HIP graph, the layer call replays to the eager call's bytes.
 
 A caller may capture whole decode steps (the reference's engine runs a layer per MLX
 graph evaluation). The layer call is stream-ordered work only: kernel launches, and
 in long-run calls with a trellis shared expert an event fork to the layer's second
 stream and a join back, with no host synchronisation, allocation or memset. Each
 replay runs after eager work of its own on the same layer and is checked bit for
-bit against the eager result.
+bit against the eager result. Two host threads calling one layer on their own
+streams and workspaces get the eager bytes too.
 """
 import numpy as np
 import pytest
@@ -57,4 +60,44 @@ def test_layer_graph_replays_equal_eager(dev, B):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
     del g
+    d.close()
+
+
+def test_layer_two_threads_two_streams(dev):
+    # calls on distinct streams with distinct workspaces may run concurrently, from two
+    # host threads on one layer handle; at 70 rows both fork the trellis shared expert
+    # onto the layer's second stream (the handle's lock orders the forks)
+    import threading
+    cfg = small_cfg()
+    d = DeviceMoeLayer(synth.make_layer(cfg, 31), dev)
+    H, B = cfg.hidden, 70
+    xs = [torch.from_numpy(synth.activations(31 + t, f"thr.{t}", B, H).view(np.float16)).to(dev).view(B, 1, H)
+          for t in range(2)]
+    want = [d(x).clone() for x in xs]
+    torch.cuda.synchronize()
+    got = [[None] * 5 for _ in range(2)]
+    errors = []
+
+    def run(t):
+        try:
+            s = torch.cuda.Stream()
+            ws = torch.empty(d.workspace_bytes(B), dtype=torch.uint8, device=dev)
+            out = [torch.empty_like(xs[t]) for _ in range(5)]
+            with torch.cuda.stream(s):
+                for i in range(5):
+                    d(xs[t], out=out[i], ws=ws)
+            s.synchronize()
+            got[t] = out
+        except Exception as e:  # reported on the main thread
+            errors.append(e)
+
+    th = [threading.Thread(target=run, args=(t,)) for t in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errors, errors
+    for t in range(2):
+        for i in range(5):
+            assert torch.equal(got[t][i], want[t]), (t, i)
     d.close()
