@@ -260,8 +260,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run here "
-              "(the multi-GPU design is expert-parallel sharding, described in DESIGN.md)",
-              file=sys.stderr)
+              "(across GPUs the layer would shard by expert, each GPU holding E/G experts, "
+              "which is not built)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
