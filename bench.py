@@ -235,9 +235,15 @@ def cpu_baseline(layer, words, h_list, budget_s):
             break
     med = float(np.median(times))
     rows = h_list[0].shape[0]
+    # the same call on one thread, once (a bounded sample: about threads x the median)
+    t0 = time.perf_counter()
+    pyoracle.moe_layer(ocfg, experts, shared, layer.router_w, layer.bias, h_list[0], 1)
+    t1 = time.perf_counter() - t0
     return {"value": rows / med, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{len(times)} calls of one GLM-5-shaped layer at B={rows} (distinct inputs), "
-                      f"median {med * 1e3:.0f} ms/call; oracle/exl3_oracle.c, {threads} threads",
+                      f"median {med * 1e3:.0f} ms/call; oracle/exl3_oracle.c, {threads} threads; "
+                      f"one call on 1 thread: {t1 * 1e3:.0f} ms",
+            "value_1thread": rows / t1,
             "trellis_GBps": float(np.median(nbytes)) / med / 1e9}
 
 
