@@ -10,12 +10,12 @@ namespace exl3d {
 __device__ __forceinline__ float rf16d(float v) { return (float)to_f16(v); }
 
 // silu(min(g, L)) * clamp(u, -L, L), every MLX f16 op rounded (glm5_moe.cpp:66-74,
-// 369-371): sigmoid, the product with g, and the product with u each round to f16.
+// 369-371): sigmoid, the product with g, and the product with u each round to f16. The
+// clips apply whatever L is, as mx::clip does there (L = 0 gives 0; the up clip is
+// max then min, as mx::clip's bounds are applied).
 __device__ __forceinline__ float swiglu1(float g, float u, float L) {
-  if (L > 0.0f) {
-    g = fminf(g, L);
-    u = fminf(fmaxf(u, -L), L);
-  }
+  g = fminf(g, L);
+  u = fminf(fmaxf(u, -L), L);
   const float sg = rf16d(1.0f / (1.0f + expf(-g)));
   const float act = rf16d(g * sg);
   return rf16d(act * u);
@@ -184,7 +184,7 @@ __device__ __forceinline__ void shared_swiglu_block(const float *dsh_gu, int64_t
   const float *pg = dsh_gu + i * kDenseSlots, *pu = dsh_gu + (n + i) * kDenseSlots;
   const float g0 = dense_slots_sum(pg, S), g1 = dense_slots_sum(pg + kDenseSlots, S);
   const float u0 = dense_slots_sum(pu, S), u1 = dense_slots_sum(pu + kDenseSlots, S);
-  const float L = limit > 0.0f ? rf16d(limit) : 0.0f;
+  const float L = rf16d(limit);
   const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(swiglu1(rf16d(g0), rf16d(u0), L))) |
                      ((uint32_t)bitcast<uint16_t>(to_f16(swiglu1(rf16d(g1), rf16d(u1), L))) << 16);
   *reinterpret_cast<uint32_t *>(dsh_act + i) = o;

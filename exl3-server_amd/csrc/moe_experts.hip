@@ -469,7 +469,7 @@ __global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_m
   const int64_t slot = (shared_mode ? a.P : 0) + gw / nblk;
   const int gu_stride = n_slices(a.H / 16);       // slice positions per (slot, projection)
   const int gu_sl = a.fold ? 1 : gu_stride;        // partials to sum
-  const float L = a.swiglu_limit > 0.0f ? rf16(a.swiglu_limit) : 0.0f;
+  const float L = rf16(a.swiglu_limit);  // clipped always (glm5_moe.cpp:70-71)
   const int c = blk * 128 + 2 * lane;
   // the slice partials are loaded while the expert's scale pointers are fetched
   constexpr int kMaxSl = 8;

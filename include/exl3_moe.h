@@ -74,7 +74,8 @@ typedef struct {
   int32_t topk_group;       /* groups kept */
   int32_t norm_topk_prob;   /* bool */
   float routed_scaling_factor;
-  float swiglu_limit;       /* 0 = no clamp */
+  float swiglu_limit;       /* gate <= L, up in [-L, L] before SwiGLU, always (L = f16 of
+                               this; as glm5_moe.cpp:70-71, a limit of 0 zeroes it) */
 } exl3_moe_config;
 
 /* The MoE weights of one layer. Replaces G5Layer's MoE members (glm5.h:104-110):

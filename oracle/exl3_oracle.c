@@ -561,9 +561,9 @@ static void or_swiglu(const or_linear *g, const or_linear *u, const or_linear *d
   for (int64_t i = 0; i < rows * I; ++i) {
     double gv = or_f16_to_double(gate[i]);
     double uv = or_f16_to_double(up[i]);
-    if (gv > L) gv = L;
+    if (gv > L) gv = L;   /* mx::clip(gate, none, L) */
+    if (uv < -L) uv = -L; /* mx::clip(up, -L, L): the lower bound, then the upper */
     if (uv > L) uv = L;
-    if (uv < -L) uv = -L;
     const double sig = or_f16_to_double(or_f16_from_double(1.0 / (1.0 + exp(-gv))));
     const double act = or_f16_to_double(or_f16_from_double(gv * sig));
     gate[i] = or_f16_from_double(act * uv);

@@ -414,3 +414,74 @@ def test_layer_large_hidden_many_slices(oracle, dev):
             yc = y.view(B, -1).cpu()
             assert torch.equal(d(x[31:32].contiguous()).view(-1).cpu(), yc[31])
     d.close()
+
+
+def random_cfgs(n, seed):
+    """n seeded layer configurations over the shape space the kernels take: hidden and
+    intermediate multiples of 128, E up to 64 with optional group-limited routing,
+    top-k up to 8, every K and codebook, no / trellis / f16 shared expert."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        E = int(rng.choice([4, 8, 12, 16, 40, 64]))
+        groups = [g for g in (1, 2, 4) if E % g == 0 and E // g >= 2]
+        ng = int(rng.choice(groups))
+        tg = int(rng.integers(1, ng + 1))
+        topk = int(rng.integers(1, min(8, E * tg // ng) + 1))
+        shared = int(rng.integers(0, 3))  # 0 none, 1 trellis, 2 f16
+        out.append(synth.MoeConfig(
+            hidden=128 * int(rng.integers(1, 6)), inter=128 * int(rng.integers(1, 4)), n_experts=E,
+            top_k=topk, n_group=ng, topk_group=tg, norm_topk_prob=bool(rng.integers(0, 2)),
+            routed_scaling_factor=float(rng.choice([1.0, 1.5, 2.5])),
+            swiglu_limit=float(rng.choice([0.5, 7.0, 10.0])),
+            shared_inter=128 * int(rng.integers(1, 3)) if shared else 0,
+            gate_up_K=int(rng.integers(1, 9)), gate_up_cb=int(rng.integers(0, 3)),
+            down_K=int(rng.integers(1, 9)), down_cb=int(rng.integers(0, 3)),
+            shared_K=int(rng.integers(1, 9)) if shared == 1 else 0, shared_cb=int(rng.integers(0, 3))))
+    return out
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_layer_random_shapes(oracle, dev, i):
+    # seeded random configurations at a row count each that walks the dispatch and path
+    # boundaries: the oracle's output within tolerance, and (for the batch) one row
+    # equal to the same row alone, bit for bit
+    cfg = random_cfgs(12, 4321)[i]
+    B = (1, 3, 8, 17, 40, 70)[i % 6]
+    layer = synth.make_layer(cfg, 4400 + i)
+    d = DeviceMoeLayer(layer, dev)
+    h = synth.activations(4400 + i, f"rand.x.{i}", B, cfg.hidden)
+    x = to_dev(h, dev, B, 1, cfg.hidden)
+    y = d(x)
+    _, ids = d.route(x)
+    has_shared = cfg.shared_inter > 0
+    oc = ocfg_of(oracle, cfg, has_shared)
+    logits = oracle.router_logits(h, layer.router_w)
+    idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+    want = oracle.moe_layer_routed(oc, [l.oracle_dict() for l in layer.experts],
+                                   [l.oracle_dict() for l in layer.shared] if has_shared else None,
+                                   h, idx, w)
+    check_out(y, want)
+    r = B // 2
+    assert torch.equal(d(x[r:r + 1].contiguous()).view(-1).cpu(), y.view(B, -1).cpu()[r]), (cfg, B)
+    d.close()
+
+
+def test_swiglu_limit_zero_clips_everything(oracle, dev):
+    # the reference clips gate to <= L and up to [-L, L] whatever L is (glm5_moe.cpp:
+    # 70-71), so a limit of 0 (its default when a checkpoint has none, model.cpp:143)
+    # zeroes every expert's SwiGLU output and the layer output is exactly zero
+    cfg = synth.MoeConfig(hidden=256, inter=128, n_experts=8, top_k=2, swiglu_limit=0.0,
+                          shared_inter=128, shared_K=3, shared_cb=1)
+    layer = synth.make_layer(cfg, 77)
+    d = DeviceMoeLayer(layer, dev)
+    for B in (3, 70):
+        h = synth.activations(77, f"lim0.{B}", B, cfg.hidden)
+        y = d(to_dev(h, dev, B, 1, cfg.hidden))
+        assert torch.count_nonzero(y.float()).item() == 0, B
+    oc = ocfg_of(oracle, cfg, True)
+    h = synth.activations(77, "lim0.3", 3, cfg.hidden)
+    want, _, _ = oracle.moe_layer(oc, [l.oracle_dict() for l in layer.experts],
+                                  [l.oracle_dict() for l in layer.shared], layer.router_w, layer.bias, h)
+    assert not np.any(want.view(np.float16).astype(np.float64))
+    d.close()

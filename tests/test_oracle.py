@@ -398,3 +398,26 @@ def test_oracle_layer_rows_equal_single_rows(oracle):
     for b in range(11):
         one, _, _ = oracle.moe_layer(ocfg, ex, None, layer.router_w, layer.bias, h[b:b + 1])
         assert np.array_equal(one[0], out[b])
+
+
+def test_oracle_swiglu_clip_like_mlx(oracle):
+    # mx::clip(gate, none, L) and mx::clip(up, -L, L) apply whatever L is
+    # (glm5_moe.cpp:70-71): L = 0 zeroes the layer output; a small L bounds every
+    # SwiGLU value by L * silu(L)
+    for limit in (0.0, 0.25):
+        cfg = synth.MoeConfig(hidden=256, inter=128, n_experts=6, top_k=2, swiglu_limit=limit,
+                              shared_inter=128, gate_up_K=3, gate_up_cb=2, down_K=4, down_cb=1)
+        layer = synth.make_layer(cfg, 12)
+        h = synth.activations(12, "lim", 4, cfg.hidden)
+        ocfg = oracle.make_cfg(cfg.hidden, cfg.inter, cfg.n_experts, cfg.top_k, 1, 1, True, True,
+                               cfg.routed_scaling_factor, cfg.swiglu_limit)
+        out, idx, w = oracle.moe_layer(ocfg, [l.oracle_dict() for l in layer.experts],
+                                       [l.oracle_dict() for l in layer.shared], layer.router_w,
+                                       layer.bias, h)
+        got = out.view(np.float16).astype(np.float64)
+        want = numpy_layer(layer, h, idx, w, oracle)
+        if limit == 0.0:
+            assert not np.any(got) and not np.any(want)
+        else:
+            rms = np.sqrt(np.mean(want ** 2))
+            assert rms > 1e-4 and np.max(np.abs(got - want)) <= 2e-2 * rms
