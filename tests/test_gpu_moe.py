@@ -441,12 +441,12 @@ def random_cfgs(n, seed):
     return out
 
 
-@pytest.mark.parametrize("i", range(12))
+@pytest.mark.parametrize("i", range(24))
 def test_layer_random_shapes(oracle, dev, i):
     # seeded random configurations at a row count each that walks the dispatch and path
     # boundaries: the oracle's output within tolerance, and (for the batch) one row
     # equal to the same row alone, bit for bit
-    cfg = random_cfgs(12, 4321)[i]
+    cfg = random_cfgs(24, 4321)[i]
     B = (1, 3, 8, 17, 40, 70)[i % 6]
     layer = synth.make_layer(cfg, 4400 + i)
     d = DeviceMoeLayer(layer, dev)
