@@ -172,3 +172,28 @@ def test_dword_aligned_base(dev, K, cb):
     x = x_f16(dev, 3, 1024, f"al.x.{K}")
     assert np.array_equal(bits(trellis_linear(moved, x)), bits(trellis_linear(w, x)))
     assert np.array_equal(bits(trellis_decode(moved)), bits(trellis_decode(w)))
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_linear_random_shapes(oracle, dev, i):
+    # seeded random linears (in and out multiples of 128 up to 1280, every K and
+    # codebook, 1..70 rows): the oracle's f64 linear within LIN_TOL_RMS, one row equal to
+    # that row alone, and the grouped call (this member twice) equal to the single call
+    rng = np.random.default_rng(9000 + i)
+    in_f, out_f = 128 * int(rng.integers(1, 11)), 128 * int(rng.integers(1, 11))
+    K, cb = int(rng.integers(1, 9)), int(rng.integers(0, 3))
+    rows = int(rng.choice([1, 2, 5, 16, 17, 33, 70]))
+    w, words, su, sv = make(dev, in_f, out_f, K, cb, f"rnd.{i}")
+    xb = synth.activations(SEED, f"rnd.x.{i}", rows, in_f)
+    x = torch.from_numpy(xb.view(np.float16)).to(dev)
+    got = bits(trellis_linear(w, x))
+    want = oracle.trellis_linear(words, in_f, out_f, K, cb, su, sv, xb)
+    g = got.view(np.float16).astype(np.float64)
+    r = want.view(np.float16).astype(np.float64).reshape(g.shape)
+    rms = np.sqrt(np.mean(r ** 2))
+    assert np.isfinite(g).all() and rms > 0.01, (in_f, out_f, K, cb, rows)
+    assert np.max(np.abs(g - r)) <= LIN_TOL_RMS * rms, (in_f, out_f, K, cb, rows)
+    j = rows // 2
+    assert np.array_equal(bits(trellis_linear(w, x[j:j + 1].contiguous())), got[j:j + 1])
+    grp = bits(trellis_linear_group([w, w], x))
+    assert np.array_equal(grp[0], got) and np.array_equal(grp[1], got)
