@@ -15,7 +15,11 @@
 //                      slices summed in order, the output Hadamard (svh) and the routing
 //                      weight; the ranks summed in order; + the shared expert
 // A trellis shared expert runs the gate/up, act and down kernels on one extra "run"
-// that holds every token row (three more launches).
+// that holds every token row (three more launches; in long-run calls on the layer's
+// second stream, forked after the dispatch and joined before L6).
+// Calls of 32 rows or more add k_moe_rotate before L3 (each slot's gate/up input
+// rotated once); calls of 65 rows or more take the long-run gate/up and down kernels
+// over the pass table, and calls of 256 rows or more the tiled router logits kernel.
 #pragma once
 
 #include <hip/hip_runtime.h>
