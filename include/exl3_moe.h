@@ -12,9 +12,9 @@
  * last failure on the calling thread. Nothing is thrown across the ABI. Shape and
  * geometry errors are detected on the host before any kernel is launched.
  *
- * Threading: calls are thread-safe for distinct streams and distinct handles. A
- * workspace must not be used by two in-flight calls at once (it holds that call's
- * routing, dispatch table and intermediate activations).
+ * Threading: calls are thread-safe for distinct streams, also on one handle from
+ * several threads. A workspace must not be used by two in-flight calls at once (it
+ * holds that call's routing, dispatch table and intermediate activations).
  */
 #ifndef EXL3_MOE_H
 #define EXL3_MOE_H
@@ -132,10 +132,10 @@ typedef struct {
  * the distinct experts each call streamed (each expert counted once per call). */
 typedef struct {
   int64_t calls;
-  double router_ms;     /* logits + top-k routing + expert-order dispatch (+ f16 shared gate/up) */
-  double gate_up_ms;    /* routed gate|up kernel (+ f16 shared down) */
-  double down_ms;       /* routed SwiGLU + down kernel */
-  double combine_ms;    /* weighted combine (+ a trellis shared expert) */
+  double router_ms;     /* logits + top-k routing + expert-order dispatch */
+  double gate_up_ms;    /* (input rotation +) routed gate|up (+ f16 shared gate/up) */
+  double down_ms;       /* routed SwiGLU + down (+ f16 shared SwiGLU and down) */
+  double combine_ms;    /* (a trellis shared expert on the caller's stream +) combine */
   double total_ms;
   int64_t gate_up_trellis_bytes;
   int64_t down_trellis_bytes;

@@ -1,6 +1,7 @@
 """CPU tests of the C ABI boundary: the library loads, exports every symbol the header
 declares, and host-side validation answers without touching a GPU."""
 import ctypes as C
+import os
 
 import numpy as np
 import pytest
@@ -95,3 +96,23 @@ def test_synth_generator_is_counter_based():
     assert abs(a.astype(np.float64).mean() - 32767.5) < 2000
     x = synth.normal(2, "n", (100000,))
     assert abs(x.mean()) < 0.02 and abs(x.std() - 1) < 0.02
+
+
+@pytest.mark.parametrize("compiler,std", [("gcc", "-std=c11"), ("g++", "-std=c++17")])
+def test_header_compiles_and_links(tmp_path, compiler, std):
+    # include/exl3_moe.h as a C and as a C++ translation unit, linked against the
+    # library, calling host-only entry points (the binding a C or C++ engine would add)
+    import shutil
+    import subprocess
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not available")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    exe = tmp_path / "abi_probe"
+    src = os.path.join(root, "tests", "abi_c", "abi_probe.c")
+    lang = ["-x", "c++"] if compiler == "g++" else []
+    subprocess.run([compiler, std, "-Wall", "-Wextra", "-Werror", "-I", os.path.join(root, "include"),
+                    *lang, src, "-x", "none", "-L", libdir, "-lexl3moe", f"-Wl,-rpath,{libdir}",
+                    "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True)
+    assert out.stdout.strip() == "ok"
