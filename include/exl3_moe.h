@@ -90,12 +90,14 @@ typedef struct {
 } exl3_moe_layer_desc;
 
 /* Scheduling knobs. Mirrors TrellisTuning (trellis_gemm.h:137-145): rows_per_pass is
- * the QMV row block (reference mb), mat_min_rows the staged-MFMA threshold (0 = off,
- * default 16), mat_max_rows its cap (0 = none). None of them changes an output bit
- * of the QMV path (the k-split partition is a function of the tensor shape only). */
+ * the linear's token rows per MFMA pass (the reference's mb; 1..16), mat_min_rows and
+ * mat_max_rows the reference's staged-path window (0 = off / no cap), reported by
+ * exl3_trellis_path_info. Every pass runs on the matrix cores here, so the staged
+ * window only labels calls. None of them changes an output bit (the k-split partition
+ * is a function of the tensor shape only). */
 typedef struct {
-  int32_t rows_per_pass;  /* 0 = auto (min(rows, 4)) */
-  int32_t mat_min_rows;   /* staged fp16 MFMA path for runs with >= this many rows */
+  int32_t rows_per_pass;  /* 0 = auto: min(rows, 16), one MFMA pass */
+  int32_t mat_min_rows;   /* calls of >= this many rows count as staged (default 16) */
   int32_t mat_max_rows;   /* 0 = no cap */
 } exl3_tuning;
 
