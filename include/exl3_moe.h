@@ -221,7 +221,10 @@ exl3_status exl3_trellis_linear_grouped(const exl3_trellis_desc *members, int32_
  * Trellis words and the router are referenced, not copied. Copied into device memory
  * the layer owns (so these must hold their final values at this call): every expert's
  * suh/svh, stacked by expert like G5MoePrep (glm5_moe.cpp:430-486), and an f16 shared
- * expert, transposed to (out, in) for the matrix cores (3 * hidden * SI f16). */
+ * expert, transposed to (out, in) for the matrix cores (3 * hidden * SI f16). A layer
+ * with a trellis shared expert also owns a second stream (default priority): calls of
+ * 65 rows or more run the shared expert on it, forked from and joined back into the
+ * caller's stream within the call. */
 exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_moe_config *cfg,
                                   exl3_moe_layer_t *out);
 exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer);
