@@ -177,8 +177,9 @@ def test_dword_aligned_base(dev, K, cb):
 @pytest.mark.parametrize("i", range(12))
 def test_linear_random_shapes(oracle, dev, i):
     # seeded random linears (in and out multiples of 128 up to 1280, every K and
-    # codebook, 1..70 rows): the oracle's f64 linear within LIN_TOL_RMS, one row equal to
-    # that row alone, and the grouped call (this member twice) equal to the single call
+    # codebook, 1..70 rows): the oracle's f64 linear within the f16 bound below, one row
+    # equal to that row alone, and the grouped call (this member twice) equal to the
+    # single call
     rng = np.random.default_rng(9000 + i)
     in_f, out_f = 128 * int(rng.integers(1, 11)), 128 * int(rng.integers(1, 11))
     K, cb = int(rng.integers(1, 9)), int(rng.integers(0, 3))
@@ -192,7 +193,14 @@ def test_linear_random_shapes(oracle, dev, i):
     r = want.view(np.float16).astype(np.float64).reshape(g.shape)
     rms = np.sqrt(np.mean(r ** 2))
     assert np.isfinite(g).all() and rms > 0.01, (in_f, out_f, K, cb, rows)
-    assert np.max(np.abs(g - r)) <= LIN_TOL_RMS * rms, (in_f, out_f, K, cb, rows)
+    # yhat is rounded to f16 before the output Hadamard (trellis_gemm.cpp:397-399): where
+    # the f32 GEMV lands within its error of an f16 rounding boundary that yhat moves by
+    # one ulp, and the outputs of its 128-block move by at most one ulp of their own.
+    # So: within 2 ulps of the largest output, and almost all outputs bit-identical.
+    ulp = 2.0 ** (np.floor(np.log2(np.abs(r).max())) - 10)
+    err = np.max(np.abs(g - r))
+    assert err <= 2 * ulp, (in_f, out_f, K, cb, rows, err, ulp)
+    assert np.mean(got.reshape(-1) != want.reshape(-1)) <= 0.1, (in_f, out_f, K, cb, rows)
     j = rows // 2
     assert np.array_equal(bits(trellis_linear(w, x[j:j + 1].contiguous())), got[j:j + 1])
     grp = bits(trellis_linear_group([w, w], x))
