@@ -116,3 +116,23 @@ def test_header_compiles_and_links(tmp_path, compiler, std):
                     "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True)
     assert out.stdout.strip() == "ok"
+
+
+def test_cpp_layer_probe_compiles_and_links(tmp_path):
+    # the C++ layer caller (run on a GPU by test_gpu_abi_cpp) builds against the header,
+    # the library and the HIP runtime; without arguments it prints its usage only
+    import shutil
+    import subprocess
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    if shutil.which("g++") is None or not os.path.exists(os.path.join(rocm, "include", "hip")):
+        pytest.skip("g++ or the HIP headers not available")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    exe = tmp_path / "moe_cpp_probe"
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+                    "-I", os.path.join(root, "include"), "-I", os.path.join(rocm, "include"),
+                    os.path.join(root, "tests", "abi_c", "moe_cpp_probe.cpp"),
+                    "-L", libdir, "-lexl3moe", f"-Wl,-rpath,{libdir}",
+                    "-L", os.path.join(rocm, "lib"), "-lamdhip64", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 2 and "usage" in out.stderr
