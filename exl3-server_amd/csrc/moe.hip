@@ -1190,7 +1190,7 @@ exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer) {
 }
 
 size_t exl3_moe_workspace_size(exl3_moe_layer_t layer, int64_t rows) {
-  if (!layer || rows <= 0) return 0;
+  if (!layer || rows <= 0 || rows > (1 << 24) / layer->topk) return 0;  // as exl3_moe_layer's limit
   return moe_layout(layer, rows).total;
 }
 
@@ -1262,7 +1262,8 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
                            uint16_t *out, void *workspace, size_t workspace_bytes,
                            exl3_stream_t stream) {
   if (!layer || !h || !out || B < 0 || Lq < 0) return fail(EXL3_ERR_INVALID, "bad layer arguments");
-  const int64_t N = B * Lq;
+  if (B > 0 && Lq > ((int64_t)1 << 24) / B) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
+  const int64_t N = B * Lq;  // no overflow: checked above
   if (N == 0) return EXL3_OK;
   if (N > (1 << 24) / layer->topk) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
   const MoeLayout m = moe_layout(layer, N);

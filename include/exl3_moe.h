@@ -229,7 +229,8 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
                                   exl3_moe_layer_t *out);
 exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer);
 
-/* Workspace bytes for a call with `rows` (= B * L) token rows. */
+/* Workspace bytes for a call with `rows` (= B * L) token rows; 0 when rows <= 0 or
+ * rows exceeds one call's limit (2^24 / num_experts_per_tok). */
 size_t exl3_moe_workspace_size(exl3_moe_layer_t layer, int64_t rows);
 
 /* Router only: weights (rows, top_k) f32 and ids (rows, top_k) i32 from h (rows, hidden)
@@ -256,7 +257,9 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
                            uint16_t *out, void *workspace, size_t workspace_bytes,
                            exl3_stream_t stream);
 
-/* Stage timing (exl3_moe_timing); enabling it makes each layer call synchronous. */
+/* Stage timing (exl3_moe_timing); enabling it makes each layer call synchronous. The
+ * stage events belong to the handle: timed calls must not overlap (one caller at a
+ * time while timing is on). */
 exl3_status exl3_moe_timing_enable(exl3_moe_layer_t layer, int32_t enabled);
 exl3_status exl3_moe_timing_get(exl3_moe_layer_t layer, exl3_moe_timing *out);
 exl3_status exl3_moe_timing_reset(exl3_moe_layer_t layer);

@@ -164,6 +164,27 @@ def test_repeat_calls_are_deterministic(dev):
     d.close()
 
 
+def test_layer_rejects_too_many_rows_before_launch(dev):
+    # B * L beyond one call's limit (2^24 / top_k rows), including a product that would
+    # overflow int64, is refused on the host; the workspace query answers 0 for it
+    from exl3_amd import _lib
+    cfg = synth.config_small()
+    d = DeviceMoeLayer(synth.make_layer(cfg, 8), dev)
+    L = _lib.lib()
+    limit = (1 << 24) // cfg.top_k
+    assert d.workspace_bytes(limit) > 0 and d.workspace_bytes(limit + 1) == 0
+    x = to_dev(synth.activations(8, "lim", 1, cfg.hidden), dev, 1, 1, cfg.hidden)
+    out = torch.empty_like(x)
+    for B, Lq in ((limit + 1, 1), (1 << 40, 1 << 40), (1 << 62, 4)):
+        st = L.exl3_moe_layer(d.handle, x.data_ptr(), B, Lq, out.data_ptr(), x.data_ptr(), 1, None)
+        assert st == _lib.EXL3_ERR_UNSUPPORTED, (B, Lq)
+        assert b"too many rows" in L.exl3_last_error()
+    # the handle still works
+    y = d(x).clone()
+    assert torch.equal(d(x), y)
+    d.close()
+
+
 def glm5_layer_on_device(dev, seed, tag, cfg=None, hot_experts=None, hot_bias=0.0):
     """Full-size GLM-5 layer: small tensors from numpy, trellis words on the device."""
     cfg = cfg or synth.config_glm5()
