@@ -62,59 +62,116 @@ constexpr int kPreTile = 64;
 constexpr int kPreChunk = 128;  // k per staging round
 constexpr int kPreStride = kPreChunk + 8;  // halves per staged row (16-byte pad)
 constexpr int kPreTiledMinRows = 256;
+constexpr int kPreLoads = kPreTile * (kPreChunk / 8) / 256;  // 16-byte chunks per thread per operand
+static_assert(kPreLoads == 4, "the staging registers below are four per operand");
 
+// One staging round's global loads into registers, all issued before any is used:
+// chunk c of the round is row c / cpr, k offset 8 (c % cpr); rows and experts past the
+// end load the last valid one (never stored). The loads take no branch (chunks past
+// the round's last one load that one again, unused): a load under a branch is waited
+// for before the branch ends, which would serialise them. Named native vectors, not an
+// array of HIP's uint4: carried across the rounds' loop, those are kept in scratch memory.
+struct PreRegs {
+  u32x4 a0, a1, a2, a3, b0, b1, b2, b3;
+};
+
+__device__ __forceinline__ void pre_tiled_chunk(const MoeArgs &a, int64_t r0, int e0, int kk, int cpr,
+                                                int i, u32x4 &ra, u32x4 &rb) {
+  const int c = min((int)threadIdx.x + 256 * i, kPreTile * cpr - 1);
+  const int r = c / cpr, kc = (c % cpr) * 8;
+  const int64_t row = min<int64_t>(r0 + r, a.N - 1);
+  const int e = min(e0 + r, a.E - 1);
+  ra = *reinterpret_cast<const u32x4 *>(a.h + row * a.H + kk + kc);
+  rb = *reinterpret_cast<const u32x4 *>(a.router_w + (int64_t)e * a.H + kk + kc);
+}
+
+__device__ __forceinline__ void pre_tiled_load(const MoeArgs &a, int64_t r0, int e0, int kk, int cpr,
+                                               PreRegs &g) {
+  pre_tiled_chunk(a, r0, e0, kk, cpr, 0, g.a0, g.b0);
+  pre_tiled_chunk(a, r0, e0, kk, cpr, 1, g.a1, g.b1);
+  pre_tiled_chunk(a, r0, e0, kk, cpr, 2, g.a2, g.b2);
+  pre_tiled_chunk(a, r0, e0, kk, cpr, 3, g.a3, g.b3);
+}
+
+__device__ __forceinline__ void pre_tiled_put(uint16_t *sA, uint16_t *sB, int cpr, int i,
+                                              const u32x4 &ra, const u32x4 &rb) {
+  const int c = (int)threadIdx.x + 256 * i;
+  if (c < kPreTile * cpr) {
+    const int r = c / cpr, kc = (c % cpr) * 8;
+    *reinterpret_cast<u32x4 *>(sA + r * kPreStride + kc) = ra;
+    *reinterpret_cast<u32x4 *>(sB + r * kPreStride + kc) = rb;
+  }
+}
+
+__device__ __forceinline__ void pre_tiled_store(uint16_t *sA, uint16_t *sB, int cpr, const PreRegs &g) {
+  pre_tiled_put(sA, sB, cpr, 0, g.a0, g.b0);
+  pre_tiled_put(sA, sB, cpr, 1, g.a1, g.b1);
+  pre_tiled_put(sA, sB, cpr, 2, g.a2, g.b2);
+  pre_tiled_put(sA, sB, cpr, 3, g.a3, g.b3);
+}
+
+// Staging rounds: quarter q of the split in chunks of kPreChunk k. Round s + 1's loads
+// are issued before round s's MFMAs, so a workgroup waits on one memory round trip per
+// round.
 __global__ __launch_bounds__(256) void k_moe_pre_tiled(MoeArgs a) {
   __shared__ __align__(16) uint16_t sA[kPreTile * kPreStride];
   __shared__ __align__(16) uint16_t sB[kPreTile * kPreStride];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
-  const int H = a.H, E = a.E;
+  const int H = a.H;
   const int S = dense_mfma_splits(H), sk = H / S, qk = sk / 4;  // k per quarter
   const int sp = blockIdx.x;
   const int e0 = blockIdx.y * kPreTile;
   const int64_t r0 = (int64_t)blockIdx.z * kPreTile;
   const int wr = (wave & 1) * 32, we = (wave >> 1) * 32;
+  const int n_ch = (qk + kPreChunk - 1) / kPreChunk, n_st = 4 * n_ch;
   f32x4_ acc[2][2], D[2][2];
-  for (int q = 0; q < 4; ++q) {
+  PreRegs regs;
+  // round s: quarter s / n_ch, chunk (s % n_ch); ck a multiple of 32
+  auto round_k = [&](int s, int &ck) {
+    const int q = s / n_ch, c0 = (s % n_ch) * kPreChunk;
+    ck = min(kPreChunk, qk - c0);
+    return sp * sk + q * qk + c0;
+  };
+  int ck;
+  int kk = round_k(0, ck);
+  pre_tiled_load(a, r0, e0, kk, ck / 8, regs);
+  for (int s = 0; s < n_st; ++s) {
+    const int q = s / n_ch, chunk = s % n_ch;
+    const int cur_ck = ck;
+    if (chunk == 0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) D[i][j] = f32x4_{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c0 = 0; c0 < qk; c0 += kPreChunk) {
-      const int ck = min(kPreChunk, qk - c0);  // a multiple of 32
-      const int kk = sp * sk + q * qk + c0;
-      const int cpr = ck / 8;                  // 16-byte chunks per staged row
-      // rows and experts past the end load the last valid one (never stored)
-      for (int c = threadIdx.x; c < kPreTile * cpr; c += 256) {
-        const int r = c / cpr, kc = (c % cpr) * 8;
-        const int64_t row = min<int64_t>(r0 + r, a.N - 1);
-        const int e = min(e0 + r, E - 1);
-        *reinterpret_cast<uint4 *>(sA + r * kPreStride + kc) =
-            *reinterpret_cast<const uint4 *>(a.h + row * H + kk + kc);
-        *reinterpret_cast<uint4 *>(sB + r * kPreStride + kc) =
-            *reinterpret_cast<const uint4 *>(a.router_w + (int64_t)e * H + kk + kc);
-      }
-      __syncthreads();
-      for (int st = 0; st < ck / 32; ++st) {
-        const int ko = st * 32 + 8 * g;
-        f16x8_ A[2], B[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          A[i] = *reinterpret_cast<const f16x8_ *>(sA + (wr + 16 * i + (lane & 15)) * kPreStride + ko);
-          B[i] = *reinterpret_cast<const f16x8_ *>(sB + (we + 16 * i + (lane & 15)) * kPreStride + ko);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) D[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], D[i][j], 0, 0, 0);
-      }
-      __syncthreads();
+        for (int j = 0; j < 2; ++j) D[i][j] = f32x4_{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    if (s > 0) __syncthreads();  // every wave is done reading the previous round
+    pre_tiled_store(sA, sB, cur_ck / 8, regs);
+    __syncthreads();
+    if (s + 1 < n_st) {
+      kk = round_k(s + 1, ck);
+      pre_tiled_load(a, r0, e0, kk, ck / 8, regs);
+    }
+    for (int st = 0; st < cur_ck / 32; ++st) {
+      const int ko = st * 32 + 8 * g;
+      f16x8_ A[2], B[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i) {
+        A[i] = *reinterpret_cast<const f16x8_ *>(sA + (wr + 16 * i + (lane & 15)) * kPreStride + ko);
+        B[i] = *reinterpret_cast<const f16x8_ *>(sB + (we + 16 * i + (lane & 15)) * kPreStride + ko);
+      }
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[i][j][t] = q == 0 ? D[i][j][t] : acc[i][j][t] + D[i][j][t];
+        for (int j = 0; j < 2; ++j) D[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], D[i][j], 0, 0, 0);
+    }
+    if (chunk == n_ch - 1) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[i][j][t] = q == 0 ? D[i][j][t] : acc[i][j][t] + D[i][j][t];
+    }
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -124,7 +181,7 @@ __global__ __launch_bounds__(256) void k_moe_pre_tiled(MoeArgs a) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int64_t row = r0 + wr + 16 * i + 4 * g + t;
-        if (row < a.N && e < E) a.logits[(row * E + e) * kDenseSlots + sp] = acc[i][j][t];
+        if (row < a.N && e < a.E) a.logits[(row * a.E + e) * kDenseSlots + sp] = acc[i][j][t];
       }
     }
 }
