@@ -790,8 +790,9 @@ struct exl3_moe_layer_s {
   ExpertTab *tab_dev;  // E + 1 entries
   uint16_t *scales;    // stacked suh/svh (MoeArgs::suh_s/svh_s), E + 1 entries each
   size_t scale_off[6]; // suh 0..2, svh 0..2 (f16 elements)
-  std::vector<int64_t> expert_bytes;  // trellis bytes (+ scales) per routed expert
+  std::vector<int64_t> expert_bytes;  // trellis bytes of gate + up + down per routed expert
   std::vector<int64_t> gu_bytes, dn_bytes;  // trellis bytes of gate+up / down per expert
+  exl3_tuning tuning;  // this handle's staged-path window (the diag's staged runs)
   int diag_on;
   exl3_moe_diag diag;
   int timing_on;
@@ -1188,6 +1189,7 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
       return hip_check(e2, "stacked scales");
     }
   }
+  L->tuning = tuning();
   L->diag_on = 0;
   std::memset(&L->diag, 0, sizeof(L->diag));
   L->timing_on = 0;
@@ -1349,28 +1351,54 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   // long-run calls: a trellis shared expert (under one wave of the machine on its own)
   // runs on the layer's second stream while the routed experts run on the caller's
   const bool side = a.fold && layer->side_made && side_stream_on();
+  // Every return after the fork joins the side stream back into the caller's (an
+  // unjoined fork would leave a graph capture of this call unable to end).
+  bool forked = false;
+  auto join_side = [&](bool locked) {
+    if (!forked) return;
+    forked = false;
+    std::unique_lock<std::mutex> lk(layer->mu, std::defer_lock);
+    if (!locked) lk.lock();
+    (void)hipEventRecord(layer->join, layer->side);
+    (void)hipStreamWaitEvent(st, layer->join, 0);
+  };
+  auto fail_joined = [&](exl3_status r) {
+    join_side(false);
+    return r;
+  };
   if (side) {
     // one caller at a time records the fork and join (calls on other threads and
     // streams would otherwise interleave them)
     std::lock_guard<std::mutex> lk(layer->mu);
     EXL3_HIP(hipEventRecord(layer->fork, st));
     EXL3_HIP(hipStreamWaitEvent(layer->side, layer->fork, 0));
+    forked = true;
     rc = launch_shared_trellis(layer, a, N, layer->side);
-    if (rc) return rc;
+    if (rc) {
+      join_side(true);
+      return rc;
+    }
     EXL3_HIP(hipEventRecord(layer->join, layer->side));
   }
   rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, units, a, 0, dense_sh, st);
-  if (rc) return rc;
-  if (timed) EXL3_HIP(hipEventRecord(layer->ev[2], st));
+  if (rc) return fail_joined(rc);
+  if (timed) {
+    const hipError_t e = hipEventRecord(layer->ev[2], st);
+    if (e != hipSuccess) return fail_joined(hip_check(e, "hipEventRecord"));
+  }
   // L4: routed SwiGLU activations (+ the f16 shared expert's SwiGLU), L5: routed down
   // (+ the f16 shared expert's down partials)
   rc = launch_moe_act(a, 0, dense_sh ? shared_swiglu_blocks(N, layer->SI) : 0, st);
-  if (rc) return rc;
+  if (rc) return fail_joined(rc);
   rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb, units, a, 0, dense_sh, st);
-  if (rc) return rc;
-  if (timed) EXL3_HIP(hipEventRecord(layer->ev[3], st));
+  if (rc) return fail_joined(rc);
+  if (timed) {
+    const hipError_t e = hipEventRecord(layer->ev[3], st);
+    if (e != hipSuccess) return fail_joined(hip_check(e, "hipEventRecord"));
+  }
   // a trellis shared expert: one run of every token row through the same kernels
   if (side) {
+    forked = false;
     EXL3_HIP(hipStreamWaitEvent(st, layer->join, 0));
   } else if (layer->shared == exl3m::kSharedTrellis) {
     rc = launch_shared_trellis(layer, a, N, st);
@@ -1417,11 +1445,19 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
     d.pairs += m.P;
     d.runs += nr;
     d.distinct_experts += nr;
+    // a run's weights are streamed once per pass: passes of pass_rows rows on the
+    // short-run kernels, of kLongRows rows on the long-run ones (glm5_moe.cpp:280-287
+    // counts trellis_path_info(tw, r).passes the same way); a run counts as staged by
+    // the handle's mat_min_rows/mat_max_rows window
+    const int prow = a.fold ? kLongRows : a.pass_rows;
+    const exl3_tuning &tn = layer->tuning;
     for (int i = 0; i < nr; ++i) {
       const int r = rl[i];
       d.run_hist[r >= 64 ? 64 : r] += 1;
       d.shared_bytes += layer->expert_bytes[re[i]];
-      d.streamed_bytes += layer->expert_bytes[re[i]] * ((r + 15) / 16);
+      d.streamed_bytes += layer->expert_bytes[re[i]] * ((r + prow - 1) / prow);
+      if (tn.mat_min_rows > 0 && r >= tn.mat_min_rows && (tn.mat_max_rows <= 0 || r <= tn.mat_max_rows))
+        d.staged_runs += 1;
     }
   }
   return EXL3_OK;
@@ -1457,6 +1493,20 @@ exl3_status exl3_moe_diag_get(exl3_moe_layer_t layer, exl3_moe_diag *out) {
   if (!layer || !out) return fail(EXL3_ERR_INVALID, "null argument");
   std::lock_guard<std::mutex> lk(layer->mu);
   *out = layer->diag;
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_set_tuning(exl3_moe_layer_t layer, const exl3_tuning *t) {
+  if (!layer || !t) return fail(EXL3_ERR_INVALID, "null argument");
+  std::lock_guard<std::mutex> lk(layer->mu);
+  layer->tuning = *t;
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_get_tuning(exl3_moe_layer_t layer, exl3_tuning *t) {
+  if (!layer || !t) return fail(EXL3_ERR_INVALID, "null argument");
+  std::lock_guard<std::mutex> lk(layer->mu);
+  *t = layer->tuning;
   return EXL3_OK;
 }
 

@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 #include "exl3_device.hpp"
 #include "exl3_internal.hpp"
@@ -527,15 +528,21 @@ size_t moe_down_lds(int in, int pass_rows) { return expert_lds(in, pass_rows, kD
 int moe_slices(int in) { return n_slices(in / 16); }
 
 
+// Per kernel instantiation: the one-time LDS attribute, set under std::call_once so that
+// threads making their first calls at once neither race on it nor launch before it is set.
+struct KernelAttr {
+  std::once_flag once;
+  hipError_t rc = hipSuccess;
+};
+
 template <typename Kern>
 static exl3_status launch_kernel(Kern k, dim3 blocks, unsigned threads, size_t lds, hipStream_t st,
-                                 const MoeArgs &a, int shared_mode, int dense_blocks, bool &attr_set) {
-  if (!attr_set) {
-    // above the 64 KB default; leaves room for the kernels' static LDS
-    EXL3_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 128 * 1024));
-    attr_set = true;
-  }
+                                 const MoeArgs &a, int shared_mode, int dense_blocks, KernelAttr &attr) {
+  // above the 64 KB default; leaves room for the kernels' static LDS
+  std::call_once(attr.once, [&] {
+    attr.rc = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+  });
+  if (attr.rc != hipSuccess) return hip_check(attr.rc, "hipFuncSetAttribute");
   k<<<blocks, threads, lds, st>>>(a, shared_mode, dense_blocks);
   return EXL3_OK;
 }
@@ -548,7 +555,7 @@ static exl3_status moe_go(int which, dim3 blocks, hipStream_t st, const MoeArgs 
   if (a.fold) {
     if constexpr (PD <= 2) {  // long-run kernels keep at most 2 steps in flight (VGPRs)
       const size_t lds = expert_lds(in, kLongRows, kLongThreads / 64);
-      static bool set_gu = false, set_dn = false;
+      static KernelAttr set_gu, set_dn;
       return which == 0 ? launch_kernel(k_moe_gate_up_long<K, CB, PD>, blocks, kLongThreads, lds, st,
                                         a, shared_mode, dense_blocks, set_gu)
                         : launch_kernel(k_moe_down_long<K, CB, PD>, blocks, kLongThreads, lds, st, a,
@@ -557,7 +564,7 @@ static exl3_status moe_go(int which, dim3 blocks, hipStream_t st, const MoeArgs 
       return fail(EXL3_ERR_INVALID, "long-run expert kernels take at most 2 steps in flight");
     }
   }
-  static bool set_gu = false, set_dn = false;
+  static KernelAttr set_gu, set_dn;
   return which == 0
              ? launch_kernel(k_moe_gate_up<K, CB, PD>, blocks, kGuThreads,
                              expert_lds(in, a.pass_rows, kGuThreads / 64), st, a, shared_mode,

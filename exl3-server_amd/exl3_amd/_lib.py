@@ -102,6 +102,8 @@ SIGNATURES = {
     "exl3_moe_diag_enable": (C.c_int, [vp, i32]),
     "exl3_moe_diag_get": (C.c_int, [vp, P(MoeDiag)]),
     "exl3_moe_diag_reset": (C.c_int, [vp]),
+    "exl3_moe_set_tuning": (C.c_int, [vp, P(Tuning)]),
+    "exl3_moe_get_tuning": (C.c_int, [vp, P(Tuning)]),
 }
 
 _LIB = None

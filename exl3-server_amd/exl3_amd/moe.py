@@ -13,7 +13,7 @@ import numpy as np
 import torch
 
 from . import _lib, synth
-from ._lib import LinearDesc, MoeConfig, MoeDiag, MoeLayerDesc, MoeTiming, TrellisDesc, call
+from ._lib import LinearDesc, MoeConfig, MoeDiag, MoeLayerDesc, MoeTiming, TrellisDesc, Tuning, call
 from .trellis import TrellisWeight, _stream, _workspace, f16_from_bits
 
 
@@ -186,6 +186,15 @@ class DeviceMoeLayer:
         t = MoeTiming()
         call("exl3_moe_timing_get", self.handle, C.byref(t))
         return {k: getattr(t, k) for k, _ in MoeTiming._fields_}
+
+    def set_tuning(self, rows_per_pass=0, mat_min_rows=16, mat_max_rows=0):
+        """This handle's tuning knobs (exl3_moe_set_tuning); no knob moves an output bit."""
+        call("exl3_moe_set_tuning", self.handle, C.byref(Tuning(rows_per_pass, mat_min_rows, mat_max_rows)))
+
+    def tuning(self) -> dict:
+        t = Tuning()
+        call("exl3_moe_get_tuning", self.handle, C.byref(t))
+        return {k: getattr(t, k) for k, _ in Tuning._fields_}
 
     def diag_enable(self, on=True):
         call("exl3_moe_diag_enable", self.handle, 1 if on else 0)

@@ -264,7 +264,17 @@ exl3_status exl3_moe_timing_enable(exl3_moe_layer_t layer, int32_t enabled);
 exl3_status exl3_moe_timing_get(exl3_moe_layer_t layer, exl3_moe_timing *out);
 exl3_status exl3_moe_timing_reset(exl3_moe_layer_t layer);
 
-/* MoeRowsDiag equivalents (glm5_moe.h:121-122). */
+/* The handle's own copy of the tuning knobs (TrellisTuning, trellis_gemm.h:137-145,
+ * which the reference keeps process-global). It starts as exl3_get_tuning() at
+ * exl3_moe_layer_create; its mat_min_rows/mat_max_rows window decides which runs the
+ * diagnostics count as staged. No knob changes an output bit. */
+exl3_status exl3_moe_set_tuning(exl3_moe_layer_t layer, const exl3_tuning *t);
+exl3_status exl3_moe_get_tuning(exl3_moe_layer_t layer, exl3_tuning *t);
+
+/* MoeRowsDiag equivalents (glm5_moe.h:121-122). staged_runs counts runs whose row
+ * count lies in the handle's staged window; streamed_bytes counts each run's expert
+ * bytes once per weight pass (passes of min(rows, 16) rows, or of 48 rows in calls of
+ * 65 rows or more). */
 exl3_status exl3_moe_diag_enable(exl3_moe_layer_t layer, int32_t enabled);
 exl3_status exl3_moe_diag_get(exl3_moe_layer_t layer, exl3_moe_diag *out);
 exl3_status exl3_moe_diag_reset(exl3_moe_layer_t layer);

@@ -17,7 +17,7 @@
  *   or_f16_from_double   exhaustive round trip over all 65536 f16 patterns,
  *                        midpoints between neighbours (ties-to-even), the
  *                        overflow/underflow edges, numpy.float16 as a second
- *                        implementation (tests/test_oracle_golden.py)
+ *                        implementation (tests/test_oracle.py)
  *   or_codebook_lut      golden hashes + samples written from the reference's
  *                        own exl3.cpp (tests/golden/), closed-form ranges
  *   or_decode_inner      golden outputs from the reference's decode_inner, and
@@ -27,6 +27,8 @@
  *                        the Sylvester identity H.H = 128 I
  *   or_had_pre/post      explicit Sylvester-matrix products in f64 (rounding
  *                        points checked by construction on exact inputs)
+ *   or_router_logits     numpy f64 h . W^T on a non-square layer, with the
+ *                        transposed weight layout shown to be far off
  *   or_route             the reference test's known answers (moe_test.cpp
  *                        (a)/(b)) and brute-force subset search on tiny E
  *   or_moe_runs          hand-worked sort/run cases and the (g)/(h) geometries

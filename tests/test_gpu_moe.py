@@ -289,6 +289,18 @@ def test_glm5_layer_b8_vs_oracle(oracle, dev):
     d.close()
 
 
+def check_diag_bytes(dg, run_len, cfg, pass_rows, mat_min_rows=16):
+    """MoeRowsDiag semantics (reference glm5_moe.cpp:265-287): runs in the staged window,
+    and each run's expert bytes once per weight pass (passes of pass_rows rows), from the
+    oracle's run table."""
+    run_len = [int(r) for r in run_len]
+    eb = cfg.hidden * cfg.inter * (2 * cfg.gate_up_K + cfg.down_K) // 8
+    assert dg["staged_runs"] == sum(1 for r in run_len if r >= mat_min_rows)
+    assert dg["streamed_bytes"] == sum(eb * -(-r // pass_rows) for r in run_len)
+    assert dg["shared_bytes"] == eb * len(run_len)
+    assert dg["distinct_experts"] == len(run_len)
+
+
 def test_glm5_b64_run_grouping(oracle, dev):
     # configs[3]: 48 of 64 rows identical -> 8 runs of >= 48 rows; 16 independent rows
     layer, words = glm5_layer_on_device(dev, 41, "glm5b")
@@ -311,6 +323,14 @@ def test_glm5_b64_run_grouping(oracle, dev):
     dg = d.diag()
     assert dg["run_hist"] == hist
     assert sum(1 for r in runs["run_len"] if r >= 48) >= 8
+    check_diag_bytes(dg, runs["run_len"], cfg, 16)
+    # the handle's own staged window: only the diagnostics' staged count moves
+    assert d.tuning()["mat_min_rows"] == 16
+    d.set_tuning(mat_min_rows=50)
+    d.diag_reset()
+    y2 = d(x)
+    assert torch.equal(y2.cpu(), y.cpu())
+    check_diag_bytes(d.diag(), runs["run_len"], cfg, 16, mat_min_rows=50)
     used = set(idx.reshape(-1).tolist())
     want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used),
                                    oracle_shared(layer, words), h, idx, w)
@@ -344,6 +364,7 @@ def test_prefill_2048_config5(oracle, dev):
     for r in runs["run_len"].tolist():
         hist[min(r, 64)] = hist.get(min(r, 64), 0) + 1
     assert d.diag()["run_hist"] == hist
+    check_diag_bytes(d.diag(), runs["run_len"], cfg, 48)
     # sampled rows: single-row calls (the decode path) give the same bits, and the
     # oracle agrees within the tolerance
     rows = sorted(set(list(range(0, N, 171)) + [N - 1]))

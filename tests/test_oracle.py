@@ -25,15 +25,18 @@ def sha(a):
 # --- f16 rounding (reference fp16.h:18-64) ------------------------------------------------
 
 def test_f16_roundtrip_exhaustive(oracle):
+    # every one of the 65,536 f16 patterns: f16 -> f64 equals numpy's widening, and
+    # f64 -> f16 returns the same pattern (NaNs to the canonical quiet NaN)
     L = oracle.lib()
     bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     vals = bits.view(np.float16).astype(np.float64)
-    for b, v in zip(bits[::97], vals[::97]):
-        if np.isnan(v):
-            assert L.or_f16_from_double(float(v)) == 0x7E00
-            continue
-        assert L.or_f16_from_double(float(v)) == int(b)
-        assert L.or_f16_to_double(int(b)) == v
+    back = np.array([L.or_f16_from_double(float(v)) for v in vals], np.uint32)
+    wide = np.array([L.or_f16_to_double(int(b)) for b in bits], np.float64)
+    nan = np.isnan(vals)
+    assert np.array_equal(back[~nan], bits[~nan].astype(np.uint32))
+    assert np.all(back[nan] == 0x7E00)
+    assert np.array_equal(wide[~nan], vals[~nan])
+    assert np.all(np.isnan(wide[nan]))
 
 
 def test_f16_ties_to_even_vs_numpy(oracle):
@@ -44,7 +47,7 @@ def test_f16_ties_to_even_vs_numpy(oracle):
     lo = pos[:-1].view(np.float16).astype(np.float64)
     hi = pos[1:].view(np.float16).astype(np.float64)
     probe = np.concatenate([(lo + hi) / 2, lo + (hi - lo) / 4, hi - (hi - lo) / 4])
-    probe = np.concatenate([probe, -probe])[::13]
+    probe = np.concatenate([probe, -probe])
     want = probe.astype(np.float16).view(np.uint16)
     got = np.array([L.or_f16_from_double(float(x)) for x in probe], np.uint16)
     assert np.array_equal(got, want)
@@ -266,6 +269,27 @@ def test_trellis_linear_vs_dense(oracle):
 
 
 # --- router (reference glm5_moe.cpp:16-60; tests/moe_test.cpp:225-275) ----------------------
+
+def test_router_logits_vs_numpy(oracle):
+    # logits = f32(h) . f32(router_w)^T with router_w (E, H) row-major as on disk
+    # (reference glm5_moe.cpp:127-128, glm5.cpp:506). A non-square layer, so that reading
+    # the weight as (H, E), or contracting the wrong axis, cannot pass.
+    rng = np.random.default_rng(11)
+    N, E, H = 5, 24, 384
+    h = rng.normal(size=(N, H)).astype(np.float16)
+    w = (rng.normal(size=(E, H)) * 0.02).astype(np.float16)
+    got = oracle.router_logits(h.view(np.uint16), w.view(np.uint16))
+    want = h.astype(np.float64) @ w.astype(np.float64).T
+    assert got.shape == (N, E)
+    assert np.max(np.abs(got - want)) <= 1e-12 * np.max(np.abs(want))
+    # the transposed layout (the same bytes read as (H, E)) is far off
+    wt = w.reshape(-1).reshape(H, E).astype(np.float64)
+    wrong = h.astype(np.float64) @ wt
+    assert np.max(np.abs(wrong - want)) > 0.1 * np.max(np.abs(want))
+    # row t of the logits depends on row t of h only
+    got2 = oracle.router_logits(h[2:3].view(np.uint16), w.view(np.uint16))
+    assert np.array_equal(got2[0], got[2])
+
 
 def test_router_known_answer_bias_flips(oracle):
     cfg = oracle.make_cfg(2, 3, 5, 2, 1, 1, True, True, 2.5, 10.0)
