@@ -45,6 +45,10 @@ exl3_status check_desc(const exl3_trellis_desc *w, bool need_128) {
     return fail(EXL3_ERR_INVALID, "in/out features must be positive multiples of " +
                                       std::to_string(m));
   if (need_128 && (!w->suh || !w->svh)) return fail(EXL3_ERR_INVALID, "null suh/svh");
+  // the kernels address a tensor through 32-bit buffer offsets and park unused loads
+  // at 1 GiB (past any tensor)
+  if ((int64_t)w->in_features * w->out_features / 8 * w->K >= ((int64_t)1 << 30))
+    return fail(EXL3_ERR_UNSUPPORTED, "trellis tensor of 1 GiB or more");
   return EXL3_OK;
 }
 

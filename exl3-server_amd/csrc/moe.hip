@@ -842,6 +842,23 @@ int64_t xrot_min_rows() {
   return v;
 }
 
+// 128-column blocks per short-run expert workgroup (one ring-word stream per wave over
+// the group): EXL3_MOE_ITEMS_GU / EXL3_MOE_ITEMS_DN, read once. No output bit depends on
+// them.
+int env_items(const char *name, int dflt) {
+  const char *e = std::getenv(name);
+  const int x = e ? std::atoi(e) : 0;
+  return x > 0 ? x : dflt;
+}
+int gu_items_default() {
+  static const int v = env_items("EXL3_MOE_ITEMS_GU", 2);
+  return v;
+}
+int dn_items_default() {
+  static const int v = env_items("EXL3_MOE_ITEMS_DN", 2);
+  return v;
+}
+
 MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   MoeLayout m{};
   const int H = L->H, I = L->I, E = L->E, K = L->topk, SI = L->shared ? L->SI : 0;
@@ -908,6 +925,8 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.fold = N >= long_min_rows();  // long runs: kLongRows-row passes, slices folded
   a.pass_rows = (int)std::min<int64_t>(N, 16);
   a.xrot_rows = !a.fold && N >= xrot_min_rows();
+  a.gu_items = gu_items_default();
+  a.dn_items = dn_items_default();
   a.h = h;
   a.router_w = L->router_w;
   a.router_bias = L->router_bias;

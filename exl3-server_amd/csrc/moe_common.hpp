@@ -69,6 +69,8 @@ struct MoeArgs {
   int fold;           // 1: expert kernels fold their k slices (one partial per output)
   int pass_rows;      // token rows per MFMA pass of the expert kernels (<= 16)
   int xrot_rows;      // 1: the short-run gate/up kernel copies the rows k_moe_rotate rotated
+  int gu_items;       // 128-column blocks per short-run gate/up workgroup (one k slice)
+  int dn_items;       // 128-column blocks per short-run down workgroup
   // inputs
   const uint16_t *h;          // (N, H) f16
   const uint16_t *router_w;   // (E, H) f16

@@ -50,26 +50,39 @@ __device__ __forceinline__ uint32_t pack16(float a, float b) {
 }
 __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 
+// A value every lane of the wave holds (a workgroup's run record, a staged row index),
+// moved to a scalar register so that address arithmetic on it stays scalar.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+  return (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v) |
+         ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32);
+}
+
 
 constexpr int kGuThreads = 256;
 constexpr int kDnThreads = 256;
 // Waves per SIMD the short-run expert kernels are compiled for: 7 (<= 72 VGPRs) where
-// K <= 4 fits without spills, else 6 (<= 80).
+// that fits without spills (gate/up to K = 4, down to K = 5, whose LDS staging holds
+// fewer registers), else 6 (<= 80).
 template <int K>
-constexpr int kExpertWaves = K <= 4 ? 7 : 6;
+constexpr int kGuWaves = K <= 4 ? 7 : 6;
+template <int K>
+constexpr int kDnWaves = K <= 5 ? 7 : 6;
 
 struct RunInfo {
   int e, off, len;
 };
 
-// Workgroup = (run, projection, 128-column block, k-slice of H); 4 waves, wave w owns
-// n-pair 4*cb + w. Per pass of up to 16 token rows of the run: the input Hadamard of
-// the slice's 128-blocks into LDS, then one slice per wave, raw f32 partials to yhat_gu
-// (summed in slice order by k_moe_act). Grid: x = k-slice, y = 128-column block,
-// z = dense_z planes of f16 shared-expert workgroups, then 2 * run + projection (a 3-D
-// grid, so that no wave spends VALU on dividing its block index).
+// Workgroup = (run, projection, group of gu_items 128-column blocks, k-slice of H); 4
+// waves, wave w owns n-pair 4*cb + w of each block cb of the group. Per pass of up to
+// 16 token rows of the run: the input Hadamard of the slice's 128-blocks into LDS, then
+// the slice of every block of the group in one ring-word stream per wave
+// (qmv_slice_items), raw f32 partials to yhat_gu (summed in slice order by k_moe_act).
+// Grid: x = k-slice, y = block group, z = dense_z planes of f16 shared-expert
+// workgroups, then 2 * run + projection (a 3-D grid, so that no wave spends VALU on
+// dividing its block index).
 template <int K, int CB, int PD>
-__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExpertWaves<K>, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_z) {
+__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kGuWaves<K>, 8))) void k_moe_gate_up(MoeArgs a, int shared_mode, int dense_z) {
   extern __shared__ uint32_t smem[];
   if ((int)blockIdx.z < dense_z) {
     shared_gate_up_block(a.h, a.N, a.H, a.SI, a.sh_dense[0], a.sh_dense[1], a.dsh_gu,
@@ -78,7 +91,8 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExp
   }
   const int out = shared_mode ? a.SI : a.I;
   const int k_tiles = a.H / 16, ss = slice_steps(k_tiles), n_sl = gridDim.x;
-  const int sl = blockIdx.x, cb = blockIdx.y;
+  const int sl = blockIdx.x, cb0 = blockIdx.y * a.gu_items;
+  const int items = min(a.gu_items, out / 128 - cb0);
   const int zz = blockIdx.z - dense_z;
   const int proj = zz & 1, u = zz >> 1;
   RunInfo ri;
@@ -99,72 +113,79 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(kExp
     const int4 hd = *reinterpret_cast<const int4 *>(rr);
     const ulonglong2 pp = *reinterpret_cast<const ulonglong2 *>(&rr->p[2 * proj]);
     if (u >= nruns || hd.z <= 0 || pp.x == 0 || pp.y == 0) return;
-    ri = RunInfo{hd.x, hd.y, hd.z};
-    row0 = hd.w;
-    base = reinterpret_cast<const uint32_t *>(pp.x);
-    suh = reinterpret_cast<const uint16_t *>(pp.y);
+    // the record is the workgroup's: in scalar registers
+    ri = RunInfo{uniform(hd.x), uniform(hd.y), uniform(hd.z)};
+    row0 = uniform(hd.w);
+    base = reinterpret_cast<const uint32_t *>(uniform64(pp.x));
+    suh = reinterpret_cast<const uint16_t *>(uniform64(pp.y));
   }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr bool kDup = dup_cb(CB);
+  // the wave index is uniform: in a scalar register, address arithmetic built on it
+  // stays scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int slice_k = kStepTiles * ss * 16;  // k values per slice
   const int nblk = slice_k / 128;           // a power of two (slice_steps)
   const int nblk_lg = __builtin_ctz(nblk);
-  const int xs_stride = slice_k / 2;         // words per staged row
+  const int xs_stride = staged_row_words(k_tiles, kDup);  // words per staged row
   const int k_base = sl * slice_k;
   uint32_t *xs = smem;
-  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + a.pass_rows * xs_stride) + wave * kSlotChunks;
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + a.pass_rows * xs_stride) + wave * slot_chunks(K);
 
   SliceStream<K, PD> S;
   for (int p0 = 0; p0 < ri.len; p0 += a.pass_rows) {
     const int nr = min(a.pass_rows, ri.len - p0);
     // the slice's first ring words are in flight while the rows are staged
-    S.start(base, k_tiles, out / 16, sl * kStepTiles * ss, cb * 4 + wave);
+    S.start(base, k_tiles, out / 16, sl * kStepTiles * ss, cb0 * 4 + wave);
     if (a.xrot_rows) {
       // rows already rotated by k_moe_rotate (x_rot of this projection, staged k
       // order): 16-byte copies of the slice
-      const int q_row = xs_stride / 4, q_lg = __builtin_ctz(q_row);
+      const int q_row = slice_k / 8, q_lg = __builtin_ctz(q_row);  // 16-byte chunks per row
       for (int i = threadIdx.x; i < nr * q_row; i += kGuThreads) {
         const int r = i >> q_lg, q = i & (q_row - 1);
-        reinterpret_cast<uint4 *>(xs + r * xs_stride)[q] = reinterpret_cast<const uint4 *>(
-            a.xrot + ((int64_t)(ri.off + p0 + r) * 2 + proj) * a.H + k_base)[q];
+        stage_chunk<kDup>(xs + r * xs_stride, q, reinterpret_cast<const uint4 *>(
+            a.xrot + ((int64_t)(ri.off + p0 + r) * 2 + proj) * a.H + k_base)[q]);
       }
     } else {
       for (int bi = wave; bi < nr * nblk; bi += kGuThreads / 64) {
         const int r = bi >> nblk_lg, blk = bi & (nblk - 1);
         // shared slots hold the rows in order; a run's first row is in its record
-        const int row = shared_mode ? p0 + r : (p0 + r == 0 ? row0 : a.sorted_row[ri.off + p0 + r]);
+        const int row = shared_mode ? p0 + r : (p0 + r == 0 ? row0 : uniform(a.sorted_row[ri.off + p0 + r]));
         const int kc = k_base + blk * 128 + 2 * lane;
         const uint32_t hx = *reinterpret_cast<const uint32_t *>(a.h + (int64_t)row * a.H + kc);
         const uint32_t sx = *reinterpret_cast<const uint32_t *>(suh + kc);
         float v0 = lo16(hx), v1 = hi16(hx);
         wave_had_pre(v0, v1, lo16(sx), hi16(sx));
-        stage_pair(xs + r * xs_stride, blk, lane, pack16(v0, v1));
+        stage_pair<kDup>(xs + r * xs_stride, blk, lane, pack16(v0, v1));
       }
     }
     __syncthreads();
-    f32x4 D0, D1;
-    qmv_slice_run<K, CB, PD>(S, ss, xs + min(lane & 15, nr - 1) * xs_stride, slot, D0, D1);
-    const int col = cb * 128 + wave * 32;
+    float *yp = a.yhat_gu + ((int64_t)((ri.off + p0) * 2 + proj) * n_sl + sl) * a.Imax + cb0 * 128 + wave * 32;
+    const int row_stride = 2 * n_sl * a.Imax;  // a slot's partials: well below 2^31 floats
+    qmv_slice_items<K, CB, PD>(S, ss, items, xs + min(lane & 15, nr - 1) * xs_stride, slot,
+                               [=](int it, const f32x4 &D0, const f32x4 &D1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = d_row(i);
-      if (r < nr) {
-        float *y = a.yhat_gu + ((int64_t)((ri.off + p0 + r) * 2 + proj) * n_sl + sl) * a.Imax + col;
-        y[d_col(0)] = D0[i];
-        y[d_col(1)] = D1[i];
-      }
-    }
+                                 for (int i = 0; i < 4; ++i) {
+                                   const int r = d_row(i);
+                                   if (r < nr) {
+                                     const int o = r * row_stride + it * 128;
+                                     yp[o + d_col(0)] = D0[i];
+                                     yp[o + d_col(1)] = D1[i];
+                                   }
+                                 }
+                               });
     __syncthreads();
   }
 }
 
-// Workgroup = (run, 128-column block of H, k-slice of the intermediate), 4 waves, wave w
-// owns n-pair 4*cb + w. Per pass of up to 16 token rows: the rows' rotated SwiGLU
-// outputs (k_moe_act, already in the MFMA k order) for the slice into LDS, one slice
-// per wave, raw f32 partials to yhat_dn (the output Hadamard and the routing weight
-// are applied by k_moe_combine). Grid: x = k-slice, y = 128-column block, z = dense_z
-// planes of f16 shared-expert workgroups, then the run.
+// Workgroup = (run, group of dn_items 128-column blocks of H, k-slice of the
+// intermediate), 4 waves, wave w owns n-pair 4*cb + w of each block cb of the group. Per
+// pass of up to 16 token rows: the rows' rotated SwiGLU outputs (k_moe_act, already in
+// the MFMA k order) for the slice into LDS, then the slice of every block of the group
+// in one stream per wave, raw f32 partials to yhat_dn (the output Hadamard and the
+// routing weight are applied by k_moe_combine). Grid: x = k-slice, y = block group,
+// z = dense_z planes of f16 shared-expert workgroups, then the run.
 template <int K, int CB, int PD>
-__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExpertWaves<K>, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_z) {
+__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kDnWaves<K>, 8))) void k_moe_down(MoeArgs a, int shared_mode, int dense_z) {
   extern __shared__ uint32_t smem[];
   if ((int)blockIdx.z < dense_z) {
     shared_down_block(a.dsh_act, a.N, a.H, a.SI, a.sh_dense[2], a.dsh_dn,
@@ -173,7 +194,8 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExp
   }
   const int in = shared_mode ? a.SI : a.I;
   const int k_tiles = in / 16, ss = slice_steps(k_tiles);
-  const int sl = blockIdx.x, cb = blockIdx.y, u = blockIdx.z - dense_z;
+  const int sl = blockIdx.x, cb0 = blockIdx.y * a.dn_items, u = blockIdx.z - dense_z;
+  const int items = min(a.dn_items, a.H / 128 - cb0);
   RunInfo ri;
   const uint32_t *base;
   if (shared_mode) {
@@ -186,39 +208,44 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kExp
     const int4 hd = *reinterpret_cast<const int4 *>(rr);
     const uint64_t p4 = *reinterpret_cast<const uint64_t *>(&rr->p[4]);
     if (u >= nruns || hd.z <= 0 || p4 == 0) return;
-    ri = RunInfo{hd.x, hd.y, hd.z};
-    base = reinterpret_cast<const uint32_t *>(p4);
+    ri = RunInfo{uniform(hd.x), uniform(hd.y), uniform(hd.z)};
+    base = reinterpret_cast<const uint32_t *>(uniform64(p4));
   }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr bool kDup = dup_cb(CB);
+  // the wave index is uniform: in a scalar register, address arithmetic built on it
+  // stays scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int slice_k = kStepTiles * ss * 16;
-  const int xs_stride = slice_k / 2;  // words per staged row
+  const int xs_stride = staged_row_words(k_tiles, kDup);  // words per staged row
   uint32_t *xs = smem;
-  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + a.pass_rows * xs_stride) + wave * kSlotChunks;
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + a.pass_rows * xs_stride) + wave * slot_chunks(K);
 
   SliceStream<K, PD> S;
   for (int p0 = 0; p0 < ri.len; p0 += a.pass_rows) {
     const int nr = min(a.pass_rows, ri.len - p0);
-    S.start(base, k_tiles, a.H / 16, sl * kStepTiles * ss, cb * 4 + wave);
-    const int q_row = xs_stride / 4;  // 16-byte chunks per staged row (a power of two)
+    S.start(base, k_tiles, a.H / 16, sl * kStepTiles * ss, cb0 * 4 + wave);
+    const int q_row = slice_k / 8;  // 16-byte chunks of act per row (a power of two)
     const int q_lg = __builtin_ctz(q_row);
     for (int i = threadIdx.x; i < nr * q_row; i += kDnThreads) {
       const int r = i >> q_lg, q = i & (q_row - 1);
-      reinterpret_cast<uint4 *>(xs + r * xs_stride)[q] = reinterpret_cast<const uint4 *>(
-          a.act + (int64_t)(ri.off + p0 + r) * a.Imax + sl * slice_k)[q];
+      stage_chunk<kDup>(xs + r * xs_stride, q, reinterpret_cast<const uint4 *>(
+          a.act + (int64_t)(ri.off + p0 + r) * a.Imax + sl * slice_k)[q]);
     }
     __syncthreads();
-    f32x4 D0, D1;
-    qmv_slice_run<K, CB, PD>(S, ss, xs + min(lane & 15, nr - 1) * xs_stride, slot, D0, D1);
-    const int col = cb * 128 + wave * 32;
+    float *yp = a.yhat_dn + ((int64_t)(ri.off + p0) * a.S_dn + sl) * a.H + cb0 * 128 + wave * 32;
+    const int row_stride = a.S_dn * a.H;
+    qmv_slice_items<K, CB, PD>(S, ss, items, xs + min(lane & 15, nr - 1) * xs_stride, slot,
+                               [=](int it, const f32x4 &D0, const f32x4 &D1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = d_row(i);
-      if (r < nr) {
-        float *y = a.yhat_dn + ((int64_t)(ri.off + p0 + r) * a.S_dn + sl) * a.H + col;
-        y[d_col(0)] = D0[i];
-        y[d_col(1)] = D1[i];
-      }
-    }
+                                 for (int i = 0; i < 4; ++i) {
+                                   const int r = d_row(i);
+                                   if (r < nr) {
+                                     const int o = r * row_stride + it * 128;
+                                     yp[o + d_col(0)] = D0[i];
+                                     yp[o + d_col(1)] = D1[i];
+                                   }
+                                 }
+                               });
     __syncthreads();
   }
 }
@@ -284,12 +311,13 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int wave = threadIdx.x >> 6;
   const int np = cb * kWaves + wave;
   const bool active = np < n_np;  // idle waves still stage rows and meet the barriers
+  constexpr bool kDup = dup_cb(CB);
   const int slice_k = kStepTiles * ss * 16;
-  const int xs_stride = slice_k / 2;
+  const int xs_stride = staged_row_words(k_tiles, kDup);
   uint32_t *xs = smem;
-  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * kSlotChunks;
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * slot_chunks(K);
 
-  const int q_row = xs_stride / 4;  // 16-byte chunks per staged row
+  const int q_row = slice_k / 8;  // 16-byte chunks of xrot per row
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
     f32x4 acc[kLongBlocks][2];
@@ -308,7 +336,7 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
 #pragma unroll
         for (int q = 0; q < kStageBatch; ++q) {
           const int i = i0 + q * kLongThreads;
-          if (i < items) reinterpret_cast<uint4 *>(xs + (i / q_row) * xs_stride)[i % q_row] = c[q];
+          if (i < items) stage_chunk<kDup>(xs + (i / q_row) * xs_stride, i % q_row, c[q]);
         }
       }
       __syncthreads();
@@ -356,11 +384,12 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int wave = threadIdx.x >> 6;
   const int np = cb * kWaves + wave;
   const bool active = np < n_np;
+  constexpr bool kDup = dup_cb(CB);
   const int slice_k = kStepTiles * ss * 16;
-  const int xs_stride = slice_k / 2;
-  const int q_row = xs_stride / 4;  // 16-byte chunks per staged row
+  const int xs_stride = staged_row_words(k_tiles, kDup);
+  const int q_row = slice_k / 8;  // 16-byte chunks of act per row
   uint32_t *xs = smem;
-  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * kSlotChunks;
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * slot_chunks(K);
 
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
@@ -378,7 +407,7 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
 #pragma unroll
         for (int q = 0; q < kStageBatch; ++q) {
           const int i = i0 + q * kLongThreads;
-          if (i < items) reinterpret_cast<uint4 *>(xs + (i / q_row) * xs_stride)[i % q_row] = c[q];
+          if (i < items) stage_chunk<kDup>(xs + (i / q_row) * xs_stride, i % q_row, c[q]);
         }
       }
       __syncthreads();
@@ -444,7 +473,7 @@ __global__ __launch_bounds__(256) void k_moe_rotate(MoeArgs a, int n_slots) {
     wave_had_pre_n<kRotBatch>(v0, v1, s0, s1);
 #pragma unroll
     for (int q = 0; q < kRotBatch; ++q)
-      if (b0 + q < nblk) stage_pair(out, b0 + q, lane, pack16(v0[q], v1[q]));
+      if (b0 + q < nblk) stage_pair<false>(out, b0 + q, lane, pack16(v0[q], v1[q]));
   }
 }
 
@@ -509,21 +538,18 @@ __global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_m
   float a0 = swiglu1(rf16(y0[0]), rf16(y0[1]), L);
   float a1 = swiglu1(rf16(y1[0]), rf16(y1[1]), L);
   wave_had_pre(a0, a1, lo16(sud), hi16(sud));
-  stage_pair(reinterpret_cast<uint32_t *>(a.act + slot * a.Imax), blk, lane, pack16(a0, a1));
+  stage_pair<false>(reinterpret_cast<uint32_t *>(a.act + slot * a.Imax), blk, lane, pack16(a0, a1));
 }
 
 }  // namespace
 
 namespace exl3h {
 
-// Staged activation rows of one k-slice, then one ring-word slot per wave.
-static size_t expert_lds(int in, int pass_rows, int waves) {
-  const int k_tiles = in / 16;
-  return (size_t)pass_rows * (kStepTiles * slice_steps(k_tiles) * 16 / 2) * 4 +
-         (size_t)waves * kSlotChunks * 16;
+// Staged activation rows of one k-slice (in the codebook's staging form), then one
+// ring-word slot per wave.
+static size_t expert_lds(int in, int pass_rows, int waves, int K, int cb) {
+  return (size_t)pass_rows * staged_row_words(in / 16, dup_cb(cb)) * 4 + (size_t)waves * slot_chunks(K) * 16;
 }
-size_t moe_gate_up_lds(int H, int pass_rows) { return expert_lds(H, pass_rows, kGuThreads / 64); }
-size_t moe_down_lds(int in, int pass_rows) { return expert_lds(in, pass_rows, kDnThreads / 64); }
 
 int moe_slices(int in) { return n_slices(in / 16); }
 
@@ -554,7 +580,7 @@ static exl3_status moe_go(int which, dim3 blocks, hipStream_t st, const MoeArgs 
   const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
   if (a.fold) {
     if constexpr (PD <= 2) {  // long-run kernels keep at most 2 steps in flight (VGPRs)
-      const size_t lds = expert_lds(in, kLongRows, kLongThreads / 64);
+      const size_t lds = expert_lds(in, kLongRows, kLongThreads / 64, K, CB);
       static KernelAttr set_gu, set_dn;
       return which == 0 ? launch_kernel(k_moe_gate_up_long<K, CB, PD>, blocks, kLongThreads, lds, st,
                                         a, shared_mode, dense_blocks, set_gu)
@@ -567,10 +593,10 @@ static exl3_status moe_go(int which, dim3 blocks, hipStream_t st, const MoeArgs 
   static KernelAttr set_gu, set_dn;
   return which == 0
              ? launch_kernel(k_moe_gate_up<K, CB, PD>, blocks, kGuThreads,
-                             expert_lds(in, a.pass_rows, kGuThreads / 64), st, a, shared_mode,
+                             expert_lds(in, a.pass_rows, kGuThreads / 64, K, CB), st, a, shared_mode,
                              dense_blocks, set_gu)
              : launch_kernel(k_moe_down<K, CB, PD>, blocks, kDnThreads,
-                             expert_lds(in, a.pass_rows, kDnThreads / 64), st, a, shared_mode,
+                             expert_lds(in, a.pass_rows, kDnThreads / 64, K, CB), st, a, shared_mode,
                              dense_blocks, set_dn);
 }
 
@@ -607,13 +633,16 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
   const int out = which == 0 ? (shared_mode ? a.SI : a.I) : a.H;
   const int n_sl = n_slices(in / 16);
   const int waves = a.fold ? kLongThreads / 64 : kGuThreads / 64;
-  if (expert_lds(in, a.fold ? kLongRows : a.pass_rows, waves) > 128 * 1024)
+  if (expert_lds(in, a.fold ? kLongRows : a.pass_rows, waves, K, cb) > 128 * 1024)
     return fail(EXL3_ERR_UNSUPPORTED, "expert kernel LDS above 128 KB");
+  const int items = which == 0 ? a.gu_items : a.dn_items;
+  if (!a.fold && items < 1) return fail(EXL3_ERR_INVALID, "column blocks per expert workgroup below 1");
+  const int groups = (out / 128 + items - 1) / items;  // short-run: column-block groups
   int64_t blocks;
   if (a.fold)
     blocks = runs * (which == 0 ? 2 : 1) * ((out / 32 + waves - 1) / waves);
   else
-    blocks = runs * (which == 0 ? 2 : 1) * (out / 128) * n_sl;
+    blocks = runs * (which == 0 ? 2 : 1) * groups * n_sl;
   const int dense_blocks =
       !dense ? 0
              : (which == 0 ? shared_gate_up_blocks(a.N, a.H, a.SI, waves)
@@ -626,13 +655,13 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
     if (blocks > 0x7fffffff) return fail(EXL3_ERR_UNSUPPORTED, "expert launch too large");
     ub = dim3((unsigned)blocks);
   } else {
-    // x = k-slice, y = 128-column block, z = dense planes, then (run, projection)
-    const int plane = n_sl * (out / 128);
+    // x = k-slice, y = column-block group, z = dense planes, then (run, projection)
+    const int plane = n_sl * groups;
     const int dense_z = (dense_blocks + plane - 1) / plane;
     const int64_t z = runs * (which == 0 ? 2 : 1) + dense_z;
     if (z == 0) return EXL3_OK;
     if (z > 65535) return fail(EXL3_ERR_UNSUPPORTED, "expert launch too large");
-    ub = dim3((unsigned)n_sl, (unsigned)(out / 128), (unsigned)z);
+    ub = dim3((unsigned)n_sl, (unsigned)groups, (unsigned)z);
     dense_arg = dense_z;
   }
   const int pd = a.fold ? std::min(moe_prefetch(in / 16, K), 2) : moe_prefetch(in / 16, K);

@@ -141,18 +141,18 @@ __global__ __launch_bounds__(256) void k_hadamard(const uint16_t *__restrict__ x
 // slice of up to 16 xhat rows into LDS in the MFMA k order and writes the slice
 // partials part[member][slice][row][col].
 // ---------------------------------------------------------------------------------
-constexpr int kQmvSliceWords = kMaxSliceSteps * kStepTiles * 16 / 2;  // largest slice, words/row
-
 template <int K, int CB, int PD>
 __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_n, int in,
                                              int out, const uint16_t *__restrict__ xhat,
                                              int64_t x_member_stride, int64_t rows,
                                              int pass_rows, float *__restrict__ part,
                                              exl3h::PtrTable suh, int rotate) {
-  __shared__ uint32_t xs[kPassRows * kQmvSliceWords];
-  __shared__ u32x4 slots[4 * kSlotChunks];
+  constexpr bool kDup = dup_cb(CB);
+  // the largest slice's staged rows, then one ring-word slot per wave
+  __shared__ uint32_t xs[kPassRows * (kMaxSliceSteps * kStepTiles * tile_words(kDup) + 4)];
+  __shared__ u32x4 slots[4 * slot_chunks(K)];
   const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
-  const int slice_k = kStepTiles * ss * 16, xs_stride = slice_k / 2;
+  const int slice_k = kStepTiles * ss * 16, xs_stride = staged_row_words(k_tiles, kDup);
   // grid: x = 128-column block, y = row block * n_sl + k-slice, z = member (one row
   // block, the decode case, needs no division)
   const int cb = blockIdx.x;
@@ -185,25 +185,31 @@ __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_
         if (bi < items) {
           float v0 = f16_to_f32((uint16_t)(hx[q] & 0xffffu)), v1 = f16_to_f32((uint16_t)(hx[q] >> 16));
           wave_had_pre(v0, v1, f16_to_f32((uint16_t)(sx[q] & 0xffffu)), f16_to_f32((uint16_t)(sx[q] >> 16)));
-          stage_pair(xs + (bi >> nblk_lg) * xs_stride, bi & (nblk - 1), lane,
-                     (uint32_t)f32_to_f16(v0) | ((uint32_t)f32_to_f16(v1) << 16));
+          stage_pair<kDup>(xs + (bi >> nblk_lg) * xs_stride, bi & (nblk - 1), lane,
+                           (uint32_t)f32_to_f16(v0) | ((uint32_t)f32_to_f16(v1) << 16));
         }
       }
     }
   } else {
+    // xhat rows: pair w of a k-tile (k-rows 2w, 2w + 1) to its staged position
     const uint16_t *xm = xhat + member * x_member_stride + r0 * in + sl * slice_k;
-    const int xs_lg = __builtin_ctz(xs_stride);  // xs_stride = 32 * ss, a power of two
-    for (int i = threadIdx.x; i < nr * xs_stride; i += 256) {
-      const int r = i >> xs_lg, w = i & (xs_stride - 1);
-      xs[r * xs_stride + (w & ~7) + xpos(w & 7)] =
-          reinterpret_cast<const uint32_t *>(xm + (int64_t)r * in)[w];
+    const int pr_row = slice_k / 2, pr_lg = __builtin_ctz(pr_row);  // pairs per row
+    for (int i = threadIdx.x; i < nr * pr_row; i += 256) {
+      const int r = i >> pr_lg, w = i & (pr_row - 1);
+      const uint32_t v = reinterpret_cast<const uint32_t *>(xm + (int64_t)r * in)[w];
+      const int pw = (w & ~7) + xpos(w & 7);  // plain staged word
+      if constexpr (kDup) {
+        *reinterpret_cast<u32x2 *>(xs + r * xs_stride + 2 * pw) = u32x2{dup_lo(v), dup_hi(v)};
+      } else {
+        xs[r * xs_stride + pw] = v;
+      }
     }
   }
   __syncthreads();
   f32x4 D0, D1;
   qmv_slice<K, CB, PD>((const uint32_t *)trellis.p[member], k_tiles, tiles_n, sl * kStepTiles * ss,
                        cb * 4 + wave, ss, xs + min(lane & 15, nr - 1) * xs_stride,
-                       slots + wave * kSlotChunks, D0, D1);
+                       slots + wave * slot_chunks(K), D0, D1);
   float *p = part + (((int64_t)member * n_sl + sl) * rows + r0) * out + cb * 128 + wave * 32;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {

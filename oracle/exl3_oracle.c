@@ -135,6 +135,40 @@ static const uint16_t *or_lut(int cb) {
 
 void or_codebook_lut(int cb, uint16_t *lut) { memcpy(lut, or_lut(cb), sizeof(uint16_t) * 65536); }
 
+/* The GEMV's weight values, as f32. Mode 0: the reference's f16 weights. Mode 1
+ * ("exact halves"): for mcg and 3inst the exact sum lo + hi of the masked hash word's two
+ * f16 halves (exact in f32: both halves lie in [2^-3, 2), so the sum needs at most 15
+ * significant bits), i.e. the weight before the reference's f16 rounding of lo + hi
+ * (trellis_gemm.cpp:348-356). That is the value a GEMV that feeds both halves to its
+ * multiply-accumulate uses; mul1 is unchanged. */
+static float g_lutf[2][3][65536];
+static pthread_once_t g_lutf_once = PTHREAD_ONCE_INIT;
+static int g_gemv_mode = 0;
+
+float or_codebook_halves_sum(uint16_t state, int cb) {
+  const uint32_t s = state;
+  uint32_t x = (cb == 1) ? s * 0xCBAC1FEDu : s * 89226354u + 64248484u;
+  x = (x & 0x8fff8fffu) ^ 0x3b603b60u;
+  return (float)(or_f16_to_double((uint16_t)(x & 0xffffu)) + or_f16_to_double((uint16_t)(x >> 16)));
+}
+
+static void or_build_lutf(void) {
+  for (int cb = 0; cb < 3; ++cb)
+    for (uint32_t st = 0; st < 65536u; ++st) {
+      const float ref = (float)or_f16_to_double(or_lut(cb)[st]);
+      g_lutf[0][cb][st] = ref;
+      g_lutf[1][cb][st] = cb == 2 ? ref : or_codebook_halves_sum((uint16_t)st, cb);
+    }
+}
+
+static const float *or_lutf(int cb) {
+  pthread_once(&g_lutf_once, or_build_lutf);
+  return g_lutf[g_gemv_mode][cb];
+}
+
+void or_set_gemv_mode(int exact_halves) { g_gemv_mode = exact_halves ? 1 : 0; }
+int or_get_gemv_mode(void) { return g_gemv_mode; }
+
 /* ------------------------------------------------------------------------- */
 /* Tile bitstream (reference exl3.cpp:55-107; format comment exl3.h:11-16).    */
 /* One tile is 16*K stored u16; ring word i = s[2i] | s[2i+1] << 16 (8K words, */
@@ -188,11 +222,9 @@ static void or_decode_tile(const uint16_t *tile_words, int K, const uint16_t *lu
   }
 }
 
-/* Decode one tile to f32 [16][16] (row = k, col = n). */
-static void or_decode_tile_f(const uint16_t *tile_words, int K, const uint16_t *lut,
-                             float out[256]) {
-  for (int p = 0; p < 256; ++p)
-    out[or_tile_perm(p)] = (float)or_f16_to_double(lut[or_tile_state(tile_words, K, p)]);
+/* Decode one tile to f32 [16][16] (row = k, col = n) through a table of weight values. */
+static void or_decode_tile_f(const uint16_t *tile_words, int K, const float *lutf, float out[256]) {
+  for (int p = 0; p < 256; ++p) out[or_tile_perm(p)] = lutf[or_tile_state(tile_words, K, p)];
 }
 
 typedef struct {
@@ -350,7 +382,7 @@ typedef struct {
   const uint16_t *trellis;
   int64_t in, out, rows;
   int K;
-  const uint16_t *lut;
+  const float *lutf;
   const uint16_t *xhat;
   double *yhat;
 } or_mm_ctx;
@@ -364,7 +396,7 @@ static void or_mm_task(void *vctx, int64_t tn) {
   for (int64_t r = 0; r < c->rows; ++r)
     for (int col = 0; col < 16; ++col) c->yhat[r * c->out + tn * 16 + col] = 0.0;
   for (int64_t tk = 0; tk < tiles_k; ++tk) {
-    or_decode_tile_f(c->trellis + (tk * tiles_n + tn) * 16 * c->K, c->K, c->lut, w);
+    or_decode_tile_f(c->trellis + (tk * tiles_n + tn) * 16 * c->K, c->K, c->lutf, w);
     for (int64_t r = 0; r < c->rows; ++r) {
       const uint16_t *xr = c->xhat + r * c->in + tk * 16;
       double *yr = c->yhat + r * c->out + tn * 16;
@@ -380,7 +412,7 @@ static void or_mm_task(void *vctx, int64_t tn) {
 int or_matmul_raw(const uint16_t *trellis, int64_t in, int64_t out, int K, int cb,
                   const uint16_t *xhat, int64_t rows, double *yhat, int threads) {
   if (in <= 0 || out <= 0 || in % 16 || out % 16 || K < 1 || K > 8 || cb < 0 || cb > 2) return -1;
-  or_mm_ctx c = {trellis, in, out, rows, K, or_lut(cb), xhat, yhat};
+  or_mm_ctx c = {trellis, in, out, rows, K, or_lutf(cb), xhat, yhat};
   or_parallel_for(out / 16, threads, or_mm_task, &c);
   return 0;
 }

@@ -49,6 +49,13 @@ double or_f16_to_double(uint16_t h);
 uint16_t or_f16_from_double(double x);
 uint16_t or_codebook_value(uint16_t state, int cb);
 void or_codebook_lut(int cb, uint16_t *lut /* 65536 */);
+/* GEMV weight values: mode 0 = the reference's f16 weights (default); mode 1 = for
+ * mcg/3inst the exact sum of the masked hash word's two f16 halves, before the
+ * reference's f16 rounding (mul1 unchanged). Affects or_matmul_raw and everything built
+ * on it (linear, layer); decode/reconstruct always give the reference's bits. */
+void or_set_gemv_mode(int exact_halves);
+int or_get_gemv_mode(void);
+float or_codebook_halves_sum(uint16_t state, int cb);
 
 /* 16-bit state of stream position p in one tile (fast 64-bit window form and
  * a bit-by-bit form used to pin it). */

@@ -65,6 +65,10 @@ def lib():
         L.or_codebook_value.argtypes = [C.c_uint16, C.c_int]
         L.or_codebook_value.restype = C.c_uint16
         L.or_codebook_lut.argtypes = [C.c_int, u16p]
+        L.or_set_gemv_mode.argtypes = [C.c_int]
+        L.or_get_gemv_mode.restype = C.c_int
+        L.or_codebook_halves_sum.argtypes = [C.c_uint16, C.c_int]
+        L.or_codebook_halves_sum.restype = C.c_float
         L.or_tile_state.argtypes = [u16p, C.c_int, C.c_int]
         L.or_tile_state.restype = C.c_uint16
         L.or_tile_state_bruteforce.argtypes = [u16p, C.c_int, C.c_int]
@@ -121,6 +125,30 @@ def codebook_lut(cb: int) -> np.ndarray:
     out = np.zeros(65536, np.uint16)
     lib().or_codebook_lut(cb, out)
     return out
+
+
+def halves_sum_lut(cb: int) -> np.ndarray:
+    """f32 exact sum of the two f16 halves of every state's masked hash word (mcg/3inst)."""
+    L = lib()
+    return np.array([L.or_codebook_halves_sum(s, cb) for s in range(65536)], np.float32)
+
+
+class gemv_mode:
+    """Context manager: the oracle's GEMV weights inside the block. exact_halves=True
+    uses the unrounded lo + hi sum for mcg/3inst (the value the GPU GEMV multiplies),
+    False the reference's f16 weights (the default)."""
+
+    def __init__(self, exact_halves: bool):
+        self.mode = 1 if exact_halves else 0
+
+    def __enter__(self):
+        self.prev = lib().or_get_gemv_mode()
+        lib().or_set_gemv_mode(self.mode)
+        return self
+
+    def __exit__(self, *exc):
+        lib().or_set_gemv_mode(self.prev)
+        return False
 
 
 def decode_inner(trellis: np.ndarray, in_f: int, out_f: int, K: int, cb: int, threads=0):

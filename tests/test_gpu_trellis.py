@@ -1,7 +1,12 @@
 """GPU parity tests of the trellis tensor path through the C ABI.
 
 Bit-exact against the oracle: decode (W_hat), reconstruct (W), the Hadamard steps.
-Tolerance (stated per test) against the oracle's f64 GEMV: matmul_raw and linear.
+Tolerance (stated per test) against the oracle's f64 GEMV: matmul_raw and linear. For
+mcg/3inst the GEMV feeds both f16 halves of a weight's masked hash word to the matrix
+cores, i.e. multiplies the exact sum lo + hi where the reference multiplies its f16
+rounding: the tight bounds are taken against the oracle's exact-halves mode
+(oracle.gemv_mode(True)), and the reference-rounded oracle is met at the north-star
+tolerance (max |err| <= 2e-2 * rms, cosine >= 0.9999).
 Bit-exact invariants of the reference (tests/glm5_gemv_nt_test.cpp, moe_test.cpp):
 the row-block knob moves no byte, grouped == per-member, rows == single rows.
 """
@@ -86,15 +91,31 @@ def gemv_bound(xhat_bits, what_bits):
     return 64 * 2.0 ** -24 * (x @ w)
 
 
+def north_star(got_bits, want_bits):
+    g = got_bits.view(np.float16).astype(np.float64).reshape(-1)
+    r = want_bits.view(np.float16).astype(np.float64).reshape(-1)
+    rms = np.sqrt(np.mean(r ** 2))
+    cos = (g * r).sum() / np.sqrt((g ** 2).sum() * (r ** 2).sum())
+    assert np.max(np.abs(g - r)) <= 2e-2 * rms and cos >= 0.9999, (np.max(np.abs(g - r)), rms, cos)
+
+
 @pytest.mark.parametrize("K,cb", [(1, 2), (2, 0), (3, 1), (4, 1), (5, 1), (6, 0), (8, 2)])
 def test_matmul_raw_vs_f64(oracle, dev, K, cb):
     in_f, out_f, rows = 4096, 1024, 3
     w, words, _, _ = make(dev, in_f, out_f, K, cb, f"mm.{K}.{cb}")
     xh = synth.normal_f16(SEED, f"mm.x.{K}", (rows, in_f), 0.0, 1.0)
     got = trellis_matmul_raw(w, torch.from_numpy(xh.view(np.float16)).to(dev)).cpu().numpy()
+    what = oracle.decode_inner(words, in_f, out_f, K, cb)
+    bound = gemv_bound(xh, what)
+    with oracle.gemv_mode(True):
+        exact = oracle.matmul_raw(words, in_f, out_f, K, cb, xh)
+    assert np.all(np.abs(got - exact) <= bound)
+    # against the reference's f16 weights: the f32 bound plus each weight's f16 rounding
+    # (at most 2^-11 of it; none for mul1, whose weights the GEMV computes exactly)
     want = oracle.matmul_raw(words, in_f, out_f, K, cb, xh)
-    bound = gemv_bound(xh, oracle.decode_inner(words, in_f, out_f, K, cb))
-    assert np.all(np.abs(got - want) <= bound)
+    wr = 0.0 if cb == 2 else 2.0 ** -11
+    x = np.abs(xh.view(np.float16).astype(np.float64))
+    assert np.all(np.abs(got - want) <= bound + wr * (x @ np.abs(what.view(np.float16).astype(np.float64))))
 
 
 # f16 output tolerance of one linear: the f32-vs-f64 GEMV difference can move the f16
@@ -109,7 +130,9 @@ def test_linear_sweep_4096(oracle, dev, K, cb):
     w, words, su, sv = make(dev, 4096, 4096, K, cb, f"lin.{K}.{cb}")
     x = synth.activations(SEED, f"lin.x.{K}.{cb}", 1, 4096)
     got = bits(trellis_linear(w, torch.from_numpy(x.view(np.float16)).to(dev)))
-    want = oracle.trellis_linear(words, 4096, 4096, K, cb, su, sv, x)
+    north_star(got, oracle.trellis_linear(words, 4096, 4096, K, cb, su, sv, x))
+    with oracle.gemv_mode(True):
+        want = oracle.trellis_linear(words, 4096, 4096, K, cb, su, sv, x)
     g = got.view(np.float16).astype(np.float64)
     r = want.view(np.float16).astype(np.float64)
     rms = np.sqrt(np.mean(r ** 2))
@@ -177,7 +200,8 @@ def test_dword_aligned_base(dev, K, cb):
 @pytest.mark.parametrize("i", range(12))
 def test_linear_random_shapes(oracle, dev, i):
     # seeded random linears (in and out multiples of 128 up to 1280, every K and
-    # codebook, 1..70 rows): the oracle's f64 linear within the f16 bound below, one row
+    # codebook, 1..70 rows): the oracle's f64 linear (exact-halves mode) within the f16
+    # bound below and the reference-rounded one at the north-star tolerance, one row
     # equal to that row alone, and the grouped call (this member twice) equal to the
     # single call
     rng = np.random.default_rng(9000 + i)
@@ -188,7 +212,9 @@ def test_linear_random_shapes(oracle, dev, i):
     xb = synth.activations(SEED, f"rnd.x.{i}", rows, in_f)
     x = torch.from_numpy(xb.view(np.float16)).to(dev)
     got = bits(trellis_linear(w, x))
-    want = oracle.trellis_linear(words, in_f, out_f, K, cb, su, sv, xb)
+    north_star(got, oracle.trellis_linear(words, in_f, out_f, K, cb, su, sv, xb))
+    with oracle.gemv_mode(True):
+        want = oracle.trellis_linear(words, in_f, out_f, K, cb, su, sv, xb)
     g = got.view(np.float16).astype(np.float64)
     r = want.view(np.float16).astype(np.float64).reshape(g.shape)
     rms = np.sqrt(np.mean(r ** 2))

@@ -79,6 +79,47 @@ def test_codebook_golden(oracle, cb):
     assert vals.min() == g["min"] and vals.max() == g["max"]
 
 
+@pytest.mark.parametrize("cb", [0, 1])
+def test_halves_sum_rounds_to_reference(oracle, cb):
+    # the exact-halves GEMV weight is the reference weight before its one f16 rounding:
+    # RNE of it is the reference's (golden-pinned) value for every state, and it lies
+    # within half an f16 ulp of that value
+    exact = oracle.halves_sum_lut(cb).astype(np.float64)
+    ref_bits = oracle.codebook_lut(cb)
+    assert np.array_equal(exact.astype(np.float16).view(np.uint16), ref_bits)
+    ref = ref_bits.view(np.float16).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(exact - ref) <= ulp / 2)
+    assert np.any(exact != ref)  # the rounding does move some weights
+    # and it is the sum of the two halves by hand for a few states
+    C = 0xCBAC1FED if cb == 1 else 89226354
+    for st in (0, 1, 12345, 65535):
+        x = (st * C + (0 if cb == 1 else 64248484)) & 0xFFFFFFFF
+        x = (x & 0x8FFF8FFF) ^ 0x3B603B60
+        lo = np.array([x & 0xFFFF], np.uint16).view(np.float16)[0]
+        hi = np.array([x >> 16], np.uint16).view(np.float16)[0]
+        assert exact[st] == float(lo) + float(hi)
+
+
+def test_gemv_mode_switches_weights(oracle):
+    # mode 1 changes the mcg GEMV by at most the weight rounding, and mul1 not at all
+    rng = np.random.default_rng(5)
+    in_f, out_f, K = 256, 128, 3
+    tr = rng.integers(0, 65536, size=(in_f // 16, out_f // 16, 16 * K), dtype=np.uint16)
+    x = rng.normal(size=(2, in_f)).astype(np.float16).view(np.uint16)
+    for cb in (1, 2):
+        a = oracle.matmul_raw(tr, in_f, out_f, K, cb, x)
+        with oracle.gemv_mode(True):
+            b = oracle.matmul_raw(tr, in_f, out_f, K, cb, x)
+        w = oracle.decode_inner(tr, in_f, out_f, K, cb).view(np.float16).astype(np.float64)
+        bound = (np.abs(x.view(np.float16).astype(np.float64)) @ np.abs(w)) * 2.0 ** -11
+        if cb == 2:
+            assert np.array_equal(a, b)
+        else:
+            assert np.all(np.abs(a - b) <= bound) and not np.array_equal(a, b)
+    assert oracle.lib().or_get_gemv_mode() == 0
+
+
 def test_codebook_closed_form_ranges(oracle):
     # mul1: f16(0x6400 + bytesum) is an integer in [1024, 2044]; the fma maps it
     # monotonically into [1024*inv + bias, 2044*inv + bias].
