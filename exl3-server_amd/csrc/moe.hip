@@ -1336,20 +1336,109 @@ exl3_status launch_shared_trellis(const exl3_moe_layer_s *layer, const MoeArgs &
 }
 }  // namespace
 
+}  // extern "C"
+
+namespace {
+
+// Rows of one layer call (checked), or a status.
+exl3_status call_rows(exl3_moe_layer_t layer, const uint16_t *h, const uint16_t *out, int64_t B,
+                      int64_t Lq, int64_t &N) {
+  if (!layer || !h || !out || B < 0 || Lq < 0) return fail(EXL3_ERR_INVALID, "bad layer arguments");
+  if (B > 0 && Lq > ((int64_t)1 << 24) / B) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
+  N = B * Lq;  // no overflow: checked above
+  if (N > (1 << 24) / layer->topk) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
+  return EXL3_OK;
+}
+
+exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, uint16_t *out,
+                          void *workspace, const MoeLayout &m, exl3_stream_t stream, bool instrumented);
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------
+// Allocation-free calls: the workspace is this file-scope device array (one copy per
+// GPU, held until the process ends), not caller memory. Its device address is looked
+// up once per device with that device current; host code uses only that address (the
+// array's name is a host-side stand-in).
+// ---------------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  std::once_flag once;
+  hipError_t rc = hipSuccess;
+  void *ptr = nullptr;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+exl3_status scratch_of_current_device(void **ptr) {
+  int dev = 0;
+  EXL3_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(EXL3_ERR_UNSUPPORTED, "device index beyond the scratch table");
+  ScratchSlot &sl = g_scratch[dev];
+  std::call_once(sl.once, [&] {
+    void *p = nullptr;
+    sl.rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (sl.rc == hipSuccess) sl.ptr = p;
+  });
+  if (sl.rc != hipSuccess || !sl.ptr) return hip_check(sl.rc == hipSuccess ? hipErrorInvalidSymbol : sl.rc,
+                                                      "hipGetSymbolAddress(scratch)");
+  *ptr = sl.ptr;
+  return EXL3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t exl3_moe_scratch_capacity(void) { return kScratchBytes; }
+
+exl3_status exl3_moe_layer_noalloc(exl3_moe_layer_t layer, const uint16_t *h, int64_t B, int64_t L,
+                                   uint16_t *out, exl3_stream_t stream) {
+  int64_t N = 0;
+  exl3_status rc = call_rows(layer, h, out, B, L, N);
+  if (rc) return rc;
+  if (N == 0) return EXL3_OK;
+  const MoeLayout m = moe_layout(layer, N);
+  if (m.total > kScratchBytes)
+    return fail(EXL3_ERR_UNSUPPORTED, "exl3_moe_layer_noalloc: this call needs " + std::to_string(m.total) +
+                                          " bytes of workspace, above the " + std::to_string(kScratchBytes) +
+                                          "-byte scratch array (use exl3_moe_layer with a caller workspace)");
+  void *ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc) return rc;
+  return moe_layer_run(layer, h, N, out, ws, m, stream, false);
+}
+
 exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B, int64_t Lq,
                            uint16_t *out, void *workspace, size_t workspace_bytes,
                            exl3_stream_t stream) {
-  if (!layer || !h || !out || B < 0 || Lq < 0) return fail(EXL3_ERR_INVALID, "bad layer arguments");
-  if (B > 0 && Lq > ((int64_t)1 << 24) / B) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
-  const int64_t N = B * Lq;  // no overflow: checked above
-  if (N == 0) return EXL3_OK;
-  if (N > (1 << 24) / layer->topk) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
-  const MoeLayout m = moe_layout(layer, N);
-  exl3_status rc = check_ws(workspace, workspace_bytes, m.total);
+  int64_t N = 0;
+  exl3_status rc = call_rows(layer, h, out, B, Lq, N);
   if (rc) return rc;
+  if (N == 0) return EXL3_OK;
+  const MoeLayout m = moe_layout(layer, N);
+  rc = check_ws(workspace, workspace_bytes, m.total);
+  if (rc) return rc;
+  return moe_layer_run(layer, h, N, out, workspace, m, stream, true);
+}
+
+}  // extern "C"
+
+namespace {
+
+// One layer call over N token rows with its workspace. instrumented: honour the
+// handle's timing and diagnostics (both synchronise the stream; the allocation-free
+// entry point skips them).
+exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, uint16_t *out,
+                          void *workspace, const MoeLayout &m, exl3_stream_t stream, bool instrumented) {
+  exl3_status rc = EXL3_OK;
   hipStream_t st = stream_of(stream);
   const MoeArgs a = make_args(layer, m, N, h, out, (char *)workspace);
-  const bool timed = layer->timing_on != 0;
+  const bool timed = instrumented && layer->timing_on != 0;
   if (timed && !layer->ev_made) {
     for (int i = 0; i < 5; ++i) EXL3_HIP(hipEventCreate(&layer->ev[i]));
     layer->ev_made = true;
@@ -1449,7 +1538,7 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
     }
   }
 
-  if (layer->diag_on) {
+  if (instrumented && layer->diag_on) {
     std::lock_guard<std::mutex> lk(layer->mu);
     EXL3_HIP(hipStreamSynchronize(st));
     int32_t nr = 0;
@@ -1481,6 +1570,10 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
   }
   return EXL3_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 exl3_status exl3_moe_timing_enable(exl3_moe_layer_t layer, int32_t enabled) {
   if (!layer) return fail(EXL3_ERR_INVALID, "null layer");

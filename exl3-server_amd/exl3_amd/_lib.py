@@ -96,6 +96,8 @@ SIGNATURES = {
     "exl3_moe_route": (C.c_int, [vp, vp, i64, vp, vp, vp, sz, vp]),
     "exl3_moe_topk_route": (C.c_int, [vp, vp, i64, P(MoeConfig), vp, vp, vp]),
     "exl3_moe_layer": (C.c_int, [vp, vp, i64, i64, vp, vp, sz, vp]),
+    "exl3_moe_layer_noalloc": (C.c_int, [vp, vp, i64, i64, vp, vp]),
+    "exl3_moe_scratch_capacity": (sz, []),
     "exl3_moe_timing_enable": (C.c_int, [vp, i32]),
     "exl3_moe_timing_get": (C.c_int, [vp, P(MoeTiming)]),
     "exl3_moe_timing_reset": (C.c_int, [vp]),

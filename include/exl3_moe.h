@@ -257,6 +257,20 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
                            uint16_t *out, void *workspace, size_t workspace_bytes,
                            exl3_stream_t stream);
 
+/* Allocation-free form of exl3_moe_layer: no counterpart in the reference. It is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving
+ * loops that forbid hipMalloc): the workspace is a file-scope device array of the
+ * library, exl3_moe_scratch_capacity() bytes (32 MiB; enough for the GLM-5 MoE layer up
+ * to 30 token rows per call), one per GPU, held until the process ends. It calls no
+ * hipMalloc/hipFree. Calls whose exl3_moe_workspace_size() is larger return
+ * EXL3_ERR_UNSUPPORTED. Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (on different streams or threads, or different layers) race, so serialise
+ * them. Stage timing and diagnostics are not collected on this path. Outputs are
+ * bit-identical to exl3_moe_layer's. */
+exl3_status exl3_moe_layer_noalloc(exl3_moe_layer_t layer, const uint16_t *h, int64_t B, int64_t L,
+                                   uint16_t *out, exl3_stream_t stream);
+size_t exl3_moe_scratch_capacity(void);
+
 /* Stage timing (exl3_moe_timing); enabling it makes each layer call synchronous. The
  * stage events belong to the handle: timed calls must not overlap (one caller at a
  * time while timing is on). */
