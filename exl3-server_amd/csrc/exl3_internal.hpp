@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "exl3_moe.h"
 
@@ -70,5 +71,9 @@ exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, 
 exl3_status launch_qmv_finalize(int n, int n_sl, int64_t rows, int out, const float *part,
                                 float *y32, uint16_t *y16, const PtrTable &svh,
                                 hipStream_t st);
+
+// Hands device buffers made by the loader to a layer handle, which frees them at
+// exl3_moe_layer_destroy; `in_place`/`repacked` count its trellis tensors.
+void layer_adopt(exl3_moe_layer_t layer, const std::vector<void *> &bufs, int64_t in_place, int64_t repacked);
 
 }  // namespace exl3h

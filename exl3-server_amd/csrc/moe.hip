@@ -793,6 +793,8 @@ struct exl3_moe_layer_s {
   std::vector<int64_t> expert_bytes;  // trellis bytes of gate + up + down per routed expert
   std::vector<int64_t> gu_bytes, dn_bytes;  // trellis bytes of gate+up / down per expert
   exl3_tuning tuning;  // this handle's staged-path window (the diag's staged runs)
+  std::vector<void *> owned;           // device buffers of a loaded layer (exl3_moe_layer_load)
+  int64_t loaded_in_place = 0, loaded_repacked = 0;
   int diag_on;
   exl3_moe_diag diag;
   int timing_on;
@@ -806,6 +808,14 @@ struct exl3_moe_layer_s {
   bool side_made;
   std::mutex mu;
 };
+
+namespace exl3h {
+void layer_adopt(exl3_moe_layer_t layer, const std::vector<void *> &bufs, int64_t in_place, int64_t repacked) {
+  layer->owned.insert(layer->owned.end(), bufs.begin(), bufs.end());
+  layer->loaded_in_place += in_place;
+  layer->loaded_repacked += repacked;
+}
+}  // namespace exl3h
 
 namespace {
 
@@ -1239,6 +1249,8 @@ exl3_status exl3_moe_layer_create(const exl3_moe_layer_desc *desc, const exl3_mo
 
 exl3_status exl3_moe_layer_destroy(exl3_moe_layer_t layer) {
   if (!layer) return EXL3_OK;
+  for (void *p : layer->owned) (void)hipFree(p);
+  layer->owned.clear();
   if (layer->ev_made)
     for (int i = 0; i < 5; ++i) (void)hipEventDestroy(layer->ev[i]);
   if (layer->side_made) {
@@ -1605,6 +1617,13 @@ exl3_status exl3_moe_diag_get(exl3_moe_layer_t layer, exl3_moe_diag *out) {
   if (!layer || !out) return fail(EXL3_ERR_INVALID, "null argument");
   std::lock_guard<std::mutex> lk(layer->mu);
   *out = layer->diag;
+  return EXL3_OK;
+}
+
+exl3_status exl3_moe_layer_load_info(exl3_moe_layer_t layer, int64_t *in_place, int64_t *repacked) {
+  if (!layer || !in_place || !repacked) return fail(EXL3_ERR_INVALID, "null argument");
+  *in_place = layer->loaded_in_place;
+  *repacked = layer->loaded_repacked;
   return EXL3_OK;
 }
 

@@ -42,6 +42,15 @@ class MoeConfig(C.Structure):
                 ("swiglu_limit", C.c_float)]
 
 
+class StTensor(C.Structure):
+    _fields_ = [("dtype", C.c_int32), ("ndim", C.c_int32), ("shape", C.c_int64 * 8),
+                ("offset", C.c_int64), ("nbytes", C.c_int64), ("file_offset", C.c_int64)]
+
+
+ST_DTYPES = {0: "F16", 1: "BF16", 2: "F32", 3: "I16", 4: "I32", 5: "U8", 6: "I8", 7: "I64", 8: "F64",
+             9: "U16", 10: "U32", 11: "BOOL"}
+
+
 class MoeLayerDesc(C.Structure):
     _fields_ = [("experts", C.POINTER(LinearDesc)), ("shared", C.POINTER(LinearDesc)),
                 ("router_w", C.c_void_p), ("router_bias", C.c_void_p)]
@@ -105,6 +114,15 @@ SIGNATURES = {
     "exl3_moe_diag_get": (C.c_int, [vp, P(MoeDiag)]),
     "exl3_moe_diag_reset": (C.c_int, [vp]),
     "exl3_moe_set_tuning": (C.c_int, [vp, P(Tuning)]),
+    "exl3_st_open": (C.c_int, [C.c_char_p, P(vp)]),
+    "exl3_st_close": (C.c_int, [vp]),
+    "exl3_st_header_len": (i64, [vp]),
+    "exl3_st_count": (i32, [vp]),
+    "exl3_st_tensor_at": (C.c_int, [vp, i32, P(StTensor), P(C.c_char_p)]),
+    "exl3_st_find": (C.c_int, [vp, C.c_char_p, P(StTensor)]),
+    "exl3_st_data": (vp, [vp, C.c_char_p]),
+    "exl3_moe_layer_load": (C.c_int, [P(C.c_char_p), i32, C.c_char_p, P(MoeConfig), P(vp), vp]),
+    "exl3_moe_layer_load_info": (C.c_int, [vp, P(i64), P(i64)]),
     "exl3_moe_get_tuning": (C.c_int, [vp, P(Tuning)]),
 }
 

@@ -293,6 +293,59 @@ exl3_status exl3_moe_diag_enable(exl3_moe_layer_t layer, int32_t enabled);
 exl3_status exl3_moe_diag_get(exl3_moe_layer_t layer, exl3_moe_diag *out);
 exl3_status exl3_moe_diag_reset(exl3_moe_layer_t layer);
 
+/* ---------------------------------------------------------------------------------
+ * Safetensors shards and the EXL3 MoE layer loader. Replaces SafetensorsFile
+ * (safetensors.h:23-70: header parse + mmap) and the MoE part of load_glm5
+ * (glm5.cpp:284-376 load_linear, 503-518 the layer's keys). Host-only calls except
+ * exl3_moe_layer_load, which allocates and fills device memory.
+ * --------------------------------------------------------------------------------- */
+typedef enum {
+  EXL3_ST_F16 = 0, EXL3_ST_BF16 = 1, EXL3_ST_F32 = 2, EXL3_ST_I16 = 3, EXL3_ST_I32 = 4,
+  EXL3_ST_U8 = 5, EXL3_ST_I8 = 6, EXL3_ST_I64 = 7, EXL3_ST_F64 = 8, EXL3_ST_U16 = 9,
+  EXL3_ST_U32 = 10, EXL3_ST_BOOL = 11
+} exl3_st_dtype;
+
+/* One tensor of a shard (STTensor, safetensors.h:14-21). offset is relative to the data
+ * section, file_offset = header_len + offset is the byte position in the file. */
+typedef struct {
+  int32_t dtype; /* exl3_st_dtype */
+  int32_t ndim;
+  int64_t shape[8];
+  int64_t offset;
+  int64_t nbytes;
+  int64_t file_offset;
+} exl3_st_tensor;
+
+typedef struct exl3_st_file_s *exl3_st_file_t;
+
+/* Parse the header (8-byte little-endian length, JSON) and map the file read-only. The
+ * reference's consistency checks apply: dtype size x element count = byte count, and the
+ * data lies inside the file. */
+exl3_status exl3_st_open(const char *path, exl3_st_file_t *out);
+exl3_status exl3_st_close(exl3_st_file_t f);
+int64_t exl3_st_header_len(exl3_st_file_t f);  /* 8 + JSON length */
+int32_t exl3_st_count(exl3_st_file_t f);
+exl3_status exl3_st_tensor_at(exl3_st_file_t f, int32_t i, exl3_st_tensor *info, const char **name);
+exl3_status exl3_st_find(exl3_st_file_t f, const char *name, exl3_st_tensor *info);
+const void *exl3_st_data(exl3_st_file_t f, const char *name);  /* host pointer into the map */
+
+/* Load one GLM-5 MoE layer from EXL3 shards: `prefix` is the layer's "...mlp." key
+ * prefix; the keys are experts.{e}.{gate,up,down}_proj.{trellis,suh,svh,mul1|mcg},
+ * shared_experts.* (trellis or a plain f16 .weight, stored (out, in)), gate.weight (E,
+ * hidden) f16 and gate.e_score_correction_bias (E) f32. The codebook of a linear is mul1
+ * when its .mul1 marker exists, else mcg when .mcg exists, else 3inst (glm5.cpp:303).
+ * Every shard's needed byte range is copied to the device once, keeping the file's
+ * alignment modulo 4: a trellis tensor at a 4-byte-aligned file position is used in
+ * place (the reference's zero-copy view, glm5.cpp:333-347); the others are repacked on
+ * the device into aligned buffers (glm5.cpp:349-352, trellis_gemm.cpp:311-316). The
+ * returned handle owns all device memory of the layer (exl3_moe_layer_destroy frees
+ * it); the call synchronises `stream`. */
+exl3_status exl3_moe_layer_load(const char *const *shard_paths, int32_t n_shards, const char *prefix,
+                                const exl3_moe_config *cfg, exl3_moe_layer_t *out_layer,
+                                exl3_stream_t stream);
+/* For a loaded layer: trellis tensors used in place and repacked (0, 0 otherwise). */
+exl3_status exl3_moe_layer_load_info(exl3_moe_layer_t layer, int64_t *in_place, int64_t *repacked);
+
 #ifdef __cplusplus
 }
 #endif
