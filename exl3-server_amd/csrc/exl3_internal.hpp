@@ -72,6 +72,22 @@ exl3_status launch_qmv_finalize(int n, int n_sl, int64_t rows, int out, const fl
                                 float *y32, uint16_t *y16, const PtrTable &svh,
                                 hipStream_t st);
 
+// Hyper-connection prepare (csrc/hc.hip): site and shape checks, the partials' workspace,
+// and the two launches (projection partials, then finalize with the optional RMSNorm).
+exl3_status check_hc(const exl3_hc_site *hc, int D);
+inline exl3_status check_hc_shape(int n, int D) {
+  return (n < 1 || n > 4 || D <= 0 || D > 8192 || D % 2 || ((int64_t)n * D) % 256) ? EXL3_ERR_UNSUPPORTED : EXL3_OK;
+}
+size_t hc_part_bytes(int N, int D, int64_t P);
+// Whether two buffers of n bytes each share a byte.
+inline bool overlaps(const void *a, const void *b, size_t n) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return n && x < y + n && y < x + n;
+}
+exl3_status launch_hc_prepare(const exl3_hc_site *hc, const uint16_t *streams, int64_t P, int D,
+                              const uint16_t *norm_w, float norm_eps, uint16_t *out, float *post,
+                              float *comb, float *part, hipStream_t st);
+
 // Hands device buffers made by the loader to a layer handle, which frees them at
 // exl3_moe_layer_destroy; `in_place`/`repacked` count its trellis tensors.
 void layer_adopt(exl3_moe_layer_t layer, const std::vector<void *> &bufs, int64_t in_place, int64_t repacked);

@@ -735,6 +735,12 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(r0)) |
                      ((uint32_t)bitcast<uint16_t>(to_f16(r1)) << 16);
   *reinterpret_cast<uint32_t *>(a.out + (int64_t)row * a.H + c) = o;
+  if (a.hc_out) {
+    // the hyper-connection mix behind the layer (g5_hc_mix), on the f16 output
+    const int64_t so = (int64_t)row * a.hc_n * a.H + c;
+    exl3m::hc_mix_pair(a.hc_post + (int64_t)row * a.hc_n, a.hc_comb + (int64_t)row * a.hc_n * a.hc_n,
+                       a.hc_res + so, a.H, a.hc_n, lo16(o), hi16(o), a.hc_out + so);
+  }
 }
 
 // Stacks every expert's suh/svh (entry e of tab) into the layer's scale arrays: block
@@ -1362,8 +1368,17 @@ exl3_status call_rows(exl3_moe_layer_t layer, const uint16_t *h, const uint16_t 
   return EXL3_OK;
 }
 
+// The hyper-connection mix fused behind the combine (exl3_moe_block).
+struct HcEpilogue {
+  int n;
+  const float *post, *comb;
+  const uint16_t *residual;
+  uint16_t *streams_out;
+};
+
 exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, uint16_t *out,
-                          void *workspace, const MoeLayout &m, exl3_stream_t stream, bool instrumented);
+                          void *workspace, const MoeLayout &m, exl3_stream_t stream, bool instrumented,
+                          const HcEpilogue *epi = nullptr);
 
 }  // namespace
 
@@ -1425,6 +1440,68 @@ exl3_status exl3_moe_layer_noalloc(exl3_moe_layer_t layer, const uint16_t *h, in
   return moe_layer_run(layer, h, N, out, ws, m, stream, false);
 }
 
+namespace {
+// exl3_moe_block's workspace: the hyper-connection partials, the normalised rows h, post,
+// comb, the MoE output rows, then the layer call's own workspace.
+struct BlockLayout {
+  size_t part, h, post, comb, out, moe, total;
+};
+BlockLayout block_layout(exl3_moe_layer_t layer, int n, int64_t P, const MoeLayout &m) {
+  BlockLayout b{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align_up(o + bytes, 256);
+    return at;
+  };
+  b.part = take(hc_part_bytes(n, layer->H, P));
+  b.h = take(2 * (size_t)P * layer->H);
+  b.post = take(4 * (size_t)P * n);
+  b.comb = take(4 * (size_t)P * n * n);
+  b.out = take(2 * (size_t)P * layer->H);
+  b.moe = take(m.total);
+  b.total = o;
+  return b;
+}
+}  // namespace
+
+size_t exl3_moe_block_workspace_size(exl3_moe_layer_t layer, int32_t hc_mult, int64_t P) {
+  if (!layer || P < 0 || hc_mult < 1 || hc_mult > 4 || check_hc_shape(hc_mult, layer->H)) return 0;
+  if (P == 0) return 0;
+  if (P > (1 << 24) / layer->topk) return 0;
+  return block_layout(layer, hc_mult, P, moe_layout(layer, P)).total;
+}
+
+exl3_status exl3_moe_block(exl3_moe_layer_t layer, const exl3_hc_site *hc, const uint16_t *norm_w, float norm_eps,
+                           const uint16_t *streams, int64_t P, uint16_t *streams_out, void *workspace,
+                           size_t workspace_bytes, exl3_stream_t stream) {
+  if (!layer || P < 0) return fail(EXL3_ERR_INVALID, "bad block arguments");
+  exl3_status rc = check_hc(hc, layer->H);
+  if (rc) return rc;
+  if (P == 0) return EXL3_OK;
+  if (!norm_w || !streams || !streams_out) return fail(EXL3_ERR_INVALID, "null block argument");
+  if (P > (1 << 24) / layer->topk) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
+  if (reinterpret_cast<uintptr_t>(streams) % 8 || reinterpret_cast<uintptr_t>(streams_out) % 4 ||
+      reinterpret_cast<uintptr_t>(hc->fn) % 16)
+    return fail(EXL3_ERR_INVALID, "streams must be 8-byte, streams_out 4-byte and fn 16-byte aligned");
+  if (overlaps(streams, streams_out, (size_t)P * hc->mult * layer->H * 2))
+    return fail(EXL3_ERR_INVALID, "streams_out must not overlap streams");
+  const MoeLayout m = moe_layout(layer, P);
+  const BlockLayout b = block_layout(layer, hc->mult, P, m);
+  rc = check_ws(workspace, workspace_bytes, b.total);
+  if (rc) return rc;
+  char *ws = (char *)workspace;
+  uint16_t *h = (uint16_t *)(ws + b.h);
+  float *post = (float *)(ws + b.post), *comb = (float *)(ws + b.comb);
+  hipStream_t st = stream_of(stream);
+  // hc_prepare + rms_norm (glm5_forward.cpp:435-436)
+  rc = launch_hc_prepare(hc, streams, P, layer->H, norm_w, norm_eps, h, post, comb, (float *)(ws + b.part), st);
+  if (rc) return rc;
+  // moe_layer_rows (:437) with g5_hc_mix (:438) behind its combine
+  const HcEpilogue epi{hc->mult, post, comb, streams, streams_out};
+  return moe_layer_run(layer, h, P, (uint16_t *)(ws + b.out), ws + b.moe, m, stream, true, &epi);
+}
+
 exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B, int64_t Lq,
                            uint16_t *out, void *workspace, size_t workspace_bytes,
                            exl3_stream_t stream) {
@@ -1446,10 +1523,18 @@ namespace {
 // handle's timing and diagnostics (both synchronise the stream; the allocation-free
 // entry point skips them).
 exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, uint16_t *out,
-                          void *workspace, const MoeLayout &m, exl3_stream_t stream, bool instrumented) {
+                          void *workspace, const MoeLayout &m, exl3_stream_t stream, bool instrumented,
+                          const HcEpilogue *epi) {
   exl3_status rc = EXL3_OK;
   hipStream_t st = stream_of(stream);
-  const MoeArgs a = make_args(layer, m, N, h, out, (char *)workspace);
+  MoeArgs a = make_args(layer, m, N, h, out, (char *)workspace);
+  if (epi) {
+    a.hc_n = epi->n;
+    a.hc_post = epi->post;
+    a.hc_comb = epi->comb;
+    a.hc_res = epi->residual;
+    a.hc_out = epi->streams_out;
+  }
   const bool timed = instrumented && layer->timing_on != 0;
   if (timed && !layer->ev_made) {
     for (int i = 0; i < 5; ++i) EXL3_HIP(hipEventCreate(&layer->ev[i]));

@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "exl3_device.hpp"
+
 namespace exl3m {
 
 // Device-resident per-expert tensor table (the G5MoePrep equivalent, glm5.h:65-73):
@@ -109,7 +111,40 @@ struct MoeArgs {
   uint16_t *dsh_act;   // (N, SI): f16 shared expert SwiGLU output
   float *dsh_dn;       // (N, H, 8): f16 shared down k-split partials
   uint16_t *out;       // (N, H)
+  // Optional hyper-connection mix behind the combine (g5_hc_mix): with hc_out set, the
+  // combine also writes hc_out[row][n] = post[n] * out[row] + (comb^T @ residual)[n]
+  int hc_n;                 // streams N
+  const float *hc_post;     // (N_rows, hc_n) f32
+  const float *hc_comb;     // (N_rows, hc_n, hc_n) f32
+  const uint16_t *hc_res;   // (N_rows, hc_n, H) f16: the residual streams
+  uint16_t *hc_out;         // (N_rows, hc_n, H) f16: the new streams, or NULL
 };
+
+// The hyper-connection mix (glm5_hc.cpp:342-355) of two adjacent elements d, d + 1 of one
+// position, in the reference's f16 arithmetic (it runs in block_out's dtype): for every
+// stream n, f16(f16(f16(post[n]) * b) + f16(sum_m f16(comb[m][n]) * residual[m])), the
+// f16 products exact in f32 and the sum over m accumulated in f32 (a matmul's).
+// res / out point at element d of stream 0; streams are D elements apart.
+__device__ __forceinline__ void hc_mix_pair(const float *post, const float *comb, const uint16_t *res, int D, int N,
+                                            float b0, float b1, uint16_t *out) {
+  using exl3d::to_f16;
+  auto h2f = [](uint32_t v) { return exl3d::f16_to_f32((uint16_t)v); };
+  for (int n = 0; n < N; ++n) {
+    const float pn = (float)to_f16(post[n]);
+    const float a0 = (float)to_f16(pn * b0), a1 = (float)to_f16(pn * b1);
+    float r0 = 0.0f, r1 = 0.0f;
+    for (int m = 0; m < N; ++m) {
+      const float cm = (float)to_f16(comb[m * N + n]);
+      const uint32_t rv = *reinterpret_cast<const uint32_t *>(res + (int64_t)m * D);
+      r0 = fmaf(cm, h2f(rv & 0xffffu), r0);
+      r1 = fmaf(cm, h2f(rv >> 16), r1);
+    }
+    const float o0 = a0 + (float)to_f16(r0), o1 = a1 + (float)to_f16(r1);
+    *reinterpret_cast<uint32_t *>(out + (int64_t)n * D) =
+        (uint32_t)exl3d::bitcast<uint16_t>(to_f16(o0)) | ((uint32_t)exl3d::bitcast<uint16_t>(to_f16(o1)) << 16);
+  }
+}
+
 
 // Column pair (c, c + 1) summed over n partial planes in plane order, p[0] + p[1] + ...
 // (plane stride `stride` floats). MAXN planes are loaded at a time, unconditionally

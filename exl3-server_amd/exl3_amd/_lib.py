@@ -80,6 +80,11 @@ class MoeTiming(C.Structure):
                 ("gate_up_trellis_bytes", C.c_int64), ("down_trellis_bytes", C.c_int64)]
 
 
+class HcSite(C.Structure):
+    _fields_ = [("mult", C.c_int32), ("sinkhorn_iters", C.c_int32), ("eps", C.c_float),
+                ("fn", C.c_void_p), ("base", C.c_void_p), ("scale", C.c_void_p)]
+
+
 vp, i32, i64, sz = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t
 P = C.POINTER
 
@@ -124,6 +129,12 @@ SIGNATURES = {
     "exl3_moe_layer_load": (C.c_int, [P(C.c_char_p), i32, C.c_char_p, P(MoeConfig), P(vp), vp]),
     "exl3_moe_layer_load_info": (C.c_int, [vp, P(i64), P(i64)]),
     "exl3_moe_get_tuning": (C.c_int, [vp, P(Tuning)]),
+    "exl3_hc_workspace_size": (sz, [i32, i32, i64]),
+    "exl3_hc_prepare": (C.c_int, [P(HcSite), vp, i64, i32, vp, C.c_float, vp, vp, vp, vp, sz, vp]),
+    "exl3_rms_norm": (C.c_int, [vp, i64, i32, vp, C.c_float, vp, vp]),
+    "exl3_hc_mix": (C.c_int, [vp, vp, vp, vp, i64, i32, i32, vp, vp]),
+    "exl3_moe_block_workspace_size": (sz, [vp, i32, i64]),
+    "exl3_moe_block": (C.c_int, [vp, P(HcSite), vp, C.c_float, vp, i64, vp, vp, sz, vp]),
 }
 
 _LIB = None

@@ -34,7 +34,7 @@ CFLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
-SOURCES = ["trellis_kernels.hip", "moe_experts.hip", "moe.hip", "api.hip", "loader.hip"]
+SOURCES = ["trellis_kernels.hip", "moe_experts.hip", "moe.hip", "api.hip", "loader.hip", "hc.hip"]
 
 
 def _compile(src: str) -> str:

@@ -294,6 +294,55 @@ exl3_status exl3_moe_diag_get(exl3_moe_layer_t layer, exl3_moe_diag *out);
 exl3_status exl3_moe_diag_reset(exl3_moe_layer_t layer);
 
 /* ---------------------------------------------------------------------------------
+ * The steps either side of the MoE in the GLM-5 batch step (glm5_forward.cpp:434-438):
+ * hyper-connection prepare, RMSNorm, the MoE, hyper-connection mix.
+ * --------------------------------------------------------------------------------- */
+
+/* One hyper-connection site (G5Layer hc_ffn_* / hc_attn_*, glm5.h:79-82; config
+ * hc_mult, hc_sinkhorn_iters, hc_eps, model.h:65-67). fn is (W, mult*hidden) f32 with
+ * W = (2 + mult) * mult, stored (out, in) as F.linear's weight; base (W) f32; scale (3)
+ * f32. mult 1..4 (the reference's fused kernel's range). */
+typedef struct {
+  int32_t mult;
+  int32_t sinkhorn_iters;
+  float eps;
+  const float *fn;     /* device, 16-byte aligned */
+  const float *base;   /* device */
+  const float *scale;  /* device */
+} exl3_hc_site;
+
+/* Replaces g5_hc_prepare (glm5_hc.cpp:242-340) and, when norm_w != NULL, the rms_norm of
+ * its collapsed stream that follows it (glm5_attn.cpp:12-22; glm5_forward.cpp:435-436).
+ * streams (P, mult, hidden) f16 (8-byte aligned) -> out (P, hidden) f16: the collapsed
+ * stream sum_n pre[n] * streams[n], or rms_norm(collapsed) * norm_w; post (P, mult) and
+ * comb (P, mult, mult) f32 as the reference returns them. The workspace holds k-split
+ * partials (exl3_hc_workspace_size). Requires mult * hidden % 256 == 0, hidden <= 8192. */
+size_t exl3_hc_workspace_size(int32_t mult, int32_t hidden, int64_t P);
+exl3_status exl3_hc_prepare(const exl3_hc_site *hc, const uint16_t *streams, int64_t P, int32_t hidden,
+                            const uint16_t *norm_w, float norm_eps, uint16_t *out, float *post, float *comb,
+                            void *workspace, size_t workspace_bytes, exl3_stream_t stream);
+/* Replaces rms_norm (glm5_attn.cpp:12-22): y = f16(f16(x * rsqrt(mean(x^2) + eps)) * w),
+ * f32 statistics; x, y (P, hidden) f16, w (hidden) f16; hidden <= 8192. */
+exl3_status exl3_rms_norm(const uint16_t *x, int64_t P, int32_t hidden, const uint16_t *w, float eps,
+                          uint16_t *y, exl3_stream_t stream);
+/* Replaces g5_hc_mix (glm5_hc.cpp:342-355): out[p][n] = post[p][n] * block_out[p] +
+ * sum_m comb[p][m][n] * residual[p][m], in f16 as the reference (block_out's dtype). */
+exl3_status exl3_hc_mix(const uint16_t *block_out, const float *post, const float *comb, const uint16_t *residual,
+                        int64_t P, int32_t mult, int32_t hidden, uint16_t *out, exl3_stream_t stream);
+
+/* The MLP sub-block of a GLM-5 MoE layer in one call (glm5_forward.cpp:434-438):
+ * f = g5_hc_prepare(streams, hc); h = rms_norm(f.collapsed, norm_w, norm_eps);
+ * out = moe_layer_rows(h); streams_out = g5_hc_mix(out, f.post, f.comb, streams).
+ * Two launches before the MoE's own (the prepare's projection partials, then its
+ * finalize with the RMSNorm fused), and the mix fused into the MoE's combine. streams /
+ * streams_out (P, mult, hidden) f16 (distinct buffers). Bit-identical to the separate
+ * calls exl3_hc_prepare + exl3_moe_layer + exl3_hc_mix. */
+size_t exl3_moe_block_workspace_size(exl3_moe_layer_t layer, int32_t hc_mult, int64_t P);
+exl3_status exl3_moe_block(exl3_moe_layer_t layer, const exl3_hc_site *hc, const uint16_t *norm_w, float norm_eps,
+                           const uint16_t *streams, int64_t P, uint16_t *streams_out, void *workspace,
+                           size_t workspace_bytes, exl3_stream_t stream);
+
+/* ---------------------------------------------------------------------------------
  * Safetensors shards and the EXL3 MoE layer loader. Replaces SafetensorsFile
  * (safetensors.h:23-70: header parse + mmap) and the MoE part of load_glm5
  * (glm5.cpp:284-376 load_linear, 503-518 the layer's keys). Host-only calls except

@@ -682,3 +682,115 @@ int or_moe_layer(const or_moe_cfg *cfg, const or_linear *experts, const or_linea
   free(w);
   return rc;
 }
+
+/* ------------------------------------------------------------------------- */
+/* Hyper-connection prepare / mix and RMSNorm (glm5_hc.cpp:242-355,           */
+/* glm5_attn.cpp:12-22).                                                       */
+/* ------------------------------------------------------------------------- */
+
+static double or_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+void or_hc_prepare(const uint16_t *streams, int64_t P, int N, int D, const float *fn,
+                   const float *base, const float *scale, int iters, double eps,
+                   uint16_t *collapsed, double *post, double *comb) {
+  const int W = (2 + N) * N;
+  const int64_t ND = (int64_t)N * D;
+  double *w = (double *)malloc(sizeof(double) * (size_t)W);
+  double *c = (double *)malloc(sizeof(double) * (size_t)N * N);
+  double *pre = (double *)malloc(sizeof(double) * (size_t)N);
+  for (int64_t p = 0; p < P; ++p) {
+    const uint16_t *s = streams + p * ND;
+    /* 300-301: unweighted RMSNorm over the N*D axis */
+    double ss = 0.0;
+    for (int64_t i = 0; i < ND; ++i) {
+      const double v = or_f16_to_double(s[i]);
+      ss += v * v;
+    }
+    const double rms = 1.0 / sqrt(ss / (double)ND + eps);
+    /* 303: x @ fn^T, fn stored (out, in) */
+    for (int j = 0; j < W; ++j) {
+      double acc = 0.0;
+      for (int64_t i = 0; i < ND; ++i) acc += or_f16_to_double(s[i]) * rms * (double)fn[(int64_t)j * ND + i];
+      w[j] = acc;
+    }
+    /* 313-315 */
+    for (int n = 0; n < N; ++n) {
+      pre[n] = or_sigmoid(w[n] * scale[0] + base[n]) + eps;
+      post[p * N + n] = 2.0 * or_sigmoid(w[N + n] * scale[1] + base[N + n]);
+    }
+    for (int i = 0; i < N; ++i) {
+      double m = -INFINITY;
+      for (int j = 0; j < N; ++j) {
+        const double z = w[2 * N + i * N + j] * scale[2] + base[2 * N + i * N + j];
+        c[i * N + j] = z;
+        if (z > m) m = z;
+      }
+      double t = 0.0;
+      for (int j = 0; j < N; ++j) {
+        c[i * N + j] = exp(c[i * N + j] - m);
+        t += c[i * N + j];
+      }
+      for (int j = 0; j < N; ++j) c[i * N + j] = c[i * N + j] / t + eps;
+    }
+    /* 321-324: Sinkhorn, sums over axis -2 (columns) then (iters-1) x (rows, columns) */
+    for (int j = 0; j < N; ++j) {
+      double cs = 0.0;
+      for (int i = 0; i < N; ++i) cs += c[i * N + j];
+      for (int i = 0; i < N; ++i) c[i * N + j] /= (cs + eps);
+    }
+    for (int it = 0; it < iters - 1; ++it) {
+      for (int i = 0; i < N; ++i) {
+        double rs = 0.0;
+        for (int j = 0; j < N; ++j) rs += c[i * N + j];
+        for (int j = 0; j < N; ++j) c[i * N + j] /= (rs + eps);
+      }
+      for (int j = 0; j < N; ++j) {
+        double cs = 0.0;
+        for (int i = 0; i < N; ++i) cs += c[i * N + j];
+        for (int i = 0; i < N; ++i) c[i * N + j] /= (cs + eps);
+      }
+    }
+    for (int k = 0; k < N * N; ++k) comb[p * N * N + k] = c[k];
+    /* 328: collapsed = sum_n pre[n] * streams[n], in the streams' dtype */
+    for (int d = 0; d < D; ++d) {
+      double a = 0.0;
+      for (int n = 0; n < N; ++n) a += pre[n] * or_f16_to_double(s[(int64_t)n * D + d]);
+      collapsed[p * D + d] = or_f16_from_double(a);
+    }
+  }
+  free(w);
+  free(c);
+  free(pre);
+}
+
+void or_rms_norm(const uint16_t *x, int64_t P, int D, const uint16_t *w, double eps, uint16_t *y) {
+  for (int64_t p = 0; p < P; ++p) {
+    double ss = 0.0;
+    for (int d = 0; d < D; ++d) {
+      const double v = or_f16_to_double(x[p * D + d]);
+      ss += v * v;
+    }
+    const double r = 1.0 / sqrt(ss / (double)D + eps);
+    for (int d = 0; d < D; ++d) {
+      const double n = or_f16_to_double(or_f16_from_double(or_f16_to_double(x[p * D + d]) * r));
+      y[p * D + d] = or_f16_from_double(n * or_f16_to_double(w[d]));
+    }
+  }
+}
+
+void or_hc_mix(const uint16_t *block_out, const double *post, const double *comb,
+               const uint16_t *residual, int64_t P, int N, int D, uint16_t *out) {
+  for (int64_t p = 0; p < P; ++p)
+    for (int n = 0; n < N; ++n) {
+      const double pn = or_f16_to_double(or_f16_from_double(post[p * N + n]));
+      for (int d = 0; d < D; ++d) {
+        const double a = or_f16_to_double(or_f16_from_double(pn * or_f16_to_double(block_out[p * D + d])));
+        double r = 0.0;
+        for (int m = 0; m < N; ++m)
+          r += or_f16_to_double(or_f16_from_double(comb[(p * N + m) * N + n])) *
+               or_f16_to_double(residual[(p * N + m) * (int64_t)D + d]);
+        const double b = or_f16_to_double(or_f16_from_double(r));
+        out[(p * N + n) * (int64_t)D + d] = or_f16_from_double(a + b);
+      }
+    }
+}

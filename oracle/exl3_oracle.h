@@ -33,6 +33,12 @@
  *                        (a)/(b)) and brute-force subset search on tiny E
  *   or_moe_runs          hand-worked sort/run cases and the (g)/(h) geometries
  *   or_moe_layer         f64 textbook restatement on dequantised weights
+ *   or_hc_prepare        column sums of the Sinkhorn output (the last normalisation)
+ *                        equal 1, stream-permutation equivariance, invariance of
+ *                        post/comb under scaling the streams (the RMS
+ *                        normalisation), the N = 1 closed form
+ *   or_rms_norm          scale invariance and unit mean square before the weight
+ *   or_hc_mix            the N = 1 closed form and linearity in each input
  */
 #ifndef EXL3_ORACLE_H
 #define EXL3_ORACLE_H
@@ -127,6 +133,26 @@ int or_moe_layer(const or_moe_cfg *cfg, const or_linear *experts, const or_linea
 int or_moe_layer_routed(const or_moe_cfg *cfg, const or_linear *experts,
                         const or_linear *shared, const uint16_t *h, int64_t N,
                         const int32_t *idx, const double *weights, uint16_t *out, int threads);
+
+/* ------------------------------------------------------------------------- */
+/* The steps either side of the MoE in batch_step (glm5_forward.cpp:434-438):  */
+/* g5_hc_prepare (glm5_hc.cpp:242-340), rms_norm (glm5_attn.cpp:12-22) and     */
+/* g5_hc_mix (glm5_hc.cpp:342-355). f64 arithmetic with the reference's f16    */
+/* rounding points: the collapsed stream, the normalised row before its weight */
+/* multiply and after it, and the mix's product, matmul and sum.               */
+/* ------------------------------------------------------------------------- */
+
+/* streams (P, N, D) f16; fn (W, N*D) f32 with W = (2+N)*N, base (W), scale (3).
+ * Outputs: collapsed (P, D) f16, post (P, N) and comb (P, N, N) in f64. */
+void or_hc_prepare(const uint16_t *streams, int64_t P, int N, int D, const float *fn,
+                   const float *base, const float *scale, int iters, double eps,
+                   uint16_t *collapsed, double *post, double *comb);
+/* y = f16(f16(x * rsqrt(mean(x^2) + eps)) * w), x (P, D) f16, w (D) f16. */
+void or_rms_norm(const uint16_t *x, int64_t P, int D, const uint16_t *w, double eps, uint16_t *y);
+/* out[p][n][d] = f16(f16(f16(post[p][n]) * b[p][d]) + f16(sum_m f16(comb[p][m][n]) *
+ * residual[p][m][d])), all f16 (the reference runs g5_hc_mix in block_out's dtype). */
+void or_hc_mix(const uint16_t *block_out, const double *post, const double *comb,
+               const uint16_t *residual, int64_t P, int N, int D, uint16_t *out);
 
 #ifdef __cplusplus
 }

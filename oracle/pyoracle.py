@@ -92,6 +92,10 @@ def lib():
                                    f32p, u16p, C.c_int64, u16p, i32p, f64p, C.c_int]
         L.or_moe_layer_routed.argtypes = [C.POINTER(OrMoeCfg), C.POINTER(OrLinear), C.c_void_p,
                                           u16p, C.c_int64, i32p, f64p, u16p, C.c_int]
+        L.or_hc_prepare.argtypes = [u16p, C.c_int64, C.c_int, C.c_int, f32p, f32p, f32p, C.c_int,
+                                    C.c_double, u16p, f64p, f64p]
+        L.or_rms_norm.argtypes = [u16p, C.c_int64, C.c_int, u16p, C.c_double, u16p]
+        L.or_hc_mix.argtypes = [u16p, f64p, f64p, u16p, C.c_int64, C.c_int, C.c_int, u16p]
         _LIB = L
     return _LIB
 
@@ -306,4 +310,38 @@ def moe_layer_routed(cfg: OrMoeCfg, experts, shared, h, idx, weights, threads=0)
                                    out.reshape(-1), _threads(threads))
     if rc:
         raise ValueError("or_moe_layer_routed failed")
+    return out
+
+
+# --- hyper-connections and RMSNorm (glm5_hc.cpp, glm5_attn.cpp:12-22) ----------------------
+
+def hc_prepare(streams, N, D, fn, base, scale, iters, eps):
+    """streams: f16 bits (P, N, D). Returns (collapsed f16 bits (P, D), post (P, N), comb (P, N, N))."""
+    st = np.ascontiguousarray(streams, np.uint16).reshape(-1)
+    P = st.size // (N * D)
+    coll = np.zeros((P, D), np.uint16)
+    post = np.zeros((P, N), np.float64)
+    comb = np.zeros((P, N, N), np.float64)
+    lib().or_hc_prepare(st, P, N, D, np.ascontiguousarray(fn, np.float32).reshape(-1),
+                        np.ascontiguousarray(base, np.float32), np.ascontiguousarray(scale, np.float32),
+                        iters, eps, coll.reshape(-1), post.reshape(-1), comb.reshape(-1))
+    return coll, post, comb
+
+
+def rms_norm(x, w, eps):
+    x = np.ascontiguousarray(x, np.uint16)
+    P, D = x.shape
+    y = np.zeros((P, D), np.uint16)
+    lib().or_rms_norm(x.reshape(-1), P, D, np.ascontiguousarray(w, np.uint16), eps, y.reshape(-1))
+    return y
+
+
+def hc_mix(block_out, post, comb, residual):
+    b = np.ascontiguousarray(block_out, np.uint16)
+    P, D = b.shape
+    N = post.shape[1]
+    out = np.zeros((P, N, D), np.uint16)
+    lib().or_hc_mix(b.reshape(-1), np.ascontiguousarray(post, np.float64).reshape(-1),
+                    np.ascontiguousarray(comb, np.float64).reshape(-1),
+                    np.ascontiguousarray(residual, np.uint16).reshape(-1), P, N, D, out.reshape(-1))
     return out
