@@ -13,16 +13,21 @@ instances (default 8, ~15.7 GB of trellis) with their own inputs, so consecutive
 stream different experts and the 256 MB MALL cannot serve a repeated working set.
 
 --workload picks the run: glm5_moe_decode_b8 (the default and the metric's workload),
-glm5_moe_staged_b64 (configs[3]: 48 identical rows + 16 independent rows, B=64) or
-glm5_moe_prefill_2048 (configs[4]: 2048 rows, gate/up K4 3inst, down K5 mul1, K6 mcg
-shared expert, 8 hot experts taking about a quarter of the selections).
+glm5_moe_decode_b1..b4 (the same layer at 1-4 rows: decode and the multi-row verify /
+MTP regime), glm5_moe_staged_b64 (configs[3]: 48 identical rows + 16 independent rows,
+B=64), glm5_moe_prefill_2048 (configs[4]: 2048 rows, gate/up K4 3inst, down K5 mul1, K6
+mcg shared expert, 8 hot experts taking about a quarter of the selections), small_b1
+(configs[0]: hidden 512, 16 experts, top-2, K4 mcg, one row) or trellis_linear
+(configs[1]).
 
 Output: one JSON line. `value` = 8 rows / (wall time per step) with inputs resident in
 HBM. `roofline` = the routed gate|up kernel (the dominant kernel): algorithmic trellis
 bytes of the distinct experts it streams per launch / its average launch time (HIP
-events on the call's stream). `cpu_baseline` = the CPU oracle (oracle/, a C
-restatement of the same layer with on-the-fly codebook decode, threaded) on the host
-cores, on a bounded sample of the same workload.
+events on the call's stream). `cpu_baseline` (glm5_moe_decode_b8 and small_b1) = the
+f32 -O3 CPU restatement of the same layer (oracle/cpu_layer.cpp: on-the-fly table
+decode, AVX2/FMA, one worker per CPU granted to the process; routing and decoded
+weights checked bit-identical to the oracle first), median of timed calls after
+warm-up on a bounded sample of the same workload, plus one call on one thread.
 """
 from __future__ import annotations
 
@@ -55,9 +60,13 @@ def measured_traffic(kernel):
 WORKLOADS = {
     # name: (synth config, token rows per step, description)
     "glm5_moe_decode_b8": ("glm5", 8, "configs[2]: GLM-5-shaped layer, decode batch 8"),
+    **{f"glm5_moe_decode_b{b}": ("glm5", b, f"configs[2]'s layer at B={b}: decode (1) and the multi-row "
+                                            "verify / MTP regime (2-4)") for b in (1, 2, 3, 4)},
     "glm5_moe_staged_b64": ("glm5", 64, "configs[3]: 48 identical rows + 16 independent rows"),
     "glm5_moe_prefill_2048": ("prefill", 2048, "configs[4]: 2048-token prefill, gate/up K4 3inst, "
                                                "down K5 mul1, shared K6 mcg, 8 hot experts"),
+    "small_b1": ("small", 1, "configs[0]: small EXL3 MoE layer (hidden 512, 16 experts, top-2, K4 mcg), "
+                             "batch-1 decode"),
     "trellis_linear": ("linear", 1, "configs[1]: one trellis linear at rows=1 (in 4096), K=1..8 x 3 codebooks"),
 }
 
@@ -153,6 +162,10 @@ def build_layers(n_layers, seed, device, kind="glm5"):
     from exl3_amd import synth
     from exl3_amd.moe import DeviceMoeLayer, trellis_words_torch
 
+    if kind == "small":
+        cfg = synth.config_small()
+        layers = [synth.make_layer(cfg, seed + li, f"bench.small{li}") for li in range(n_layers)]
+        return cfg, [(layer, {}, DeviceMoeLayer(layer, device)) for layer in layers]
     cfg = synth.config_glm5() if kind == "glm5" else synth.config_prefill()
     H, I, E = cfg.hidden, cfg.inter, cfg.n_experts
     hot = list(range(0, E, E // 8)) if kind == "prefill" else []
@@ -204,9 +217,26 @@ def make_inputs(workload, seed, li, B, H):
     return synth.activations(seed, f"bench.x{li}", B, H)
 
 
-def cpu_baseline(layer, words, h_list, budget_s):
-    """The CPU oracle on the host cores: router + on-the-fly LUT decode + Hadamards +
-    GEMV + SwiGLU + combine + shared expert, for one layer at B rows per call."""
+def cpu_model():
+    """The host CPU's model string and logical CPU count (/proc/cpuinfo)."""
+    model, n = None, 0
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                n += 1
+                model = model or ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return model, n or os.cpu_count()
+
+
+def cpu_baseline(layer, words, h_list, budget_s, gpu_out=None):
+    """The f32 -O3 CPU restatement of the layer (oracle/cpu_layer.cpp: router, on-the-fly
+    table decode, Hadamards, f32 GEMV, SwiGLU, combine, shared expert), one worker per
+    host CPU granted to this process: two warm-up calls, then calls on distinct inputs
+    until the budget (at least 5), median; one call on one thread. Before timing, the
+    sampled call's routing is checked equal to the oracle's (f64 logits, or_route) and
+    the decoded weights of its first experts bit-equal to the oracle's decode."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -215,36 +245,66 @@ def cpu_baseline(layer, words, h_list, budget_s):
     cfg = layer.cfg
     experts = []
     for i, lin in enumerate(layer.experts):
-        experts.append(dict(trellis=words[i].cpu().numpy().view(np.uint16), suh=lin.suh, svh=lin.svh,
-                            K=lin.K, cb=lin.cb, **{"in": lin.in_f, "out": lin.out_f}))
-    shared = [l.oracle_dict() for l in layer.shared]
+        t = lin.trellis if lin.trellis is not None else words[i].cpu().numpy().view(np.uint16)
+        experts.append(dict(trellis=t, suh=lin.suh, svh=lin.svh, K=lin.K, cb=lin.cb,
+                            **{"in": lin.in_f, "out": lin.out_f}))
+    shared = [l.oracle_dict() for l in layer.shared] if layer.shared else None
     ocfg = pyoracle.make_cfg(cfg.hidden, cfg.inter, cfg.n_experts, cfg.top_k, cfg.n_group,
-                             cfg.topk_group, cfg.norm_topk_prob, True, cfg.routed_scaling_factor,
-                             cfg.swiglu_limit)
-    threads = pyoracle._threads(0)
+                             cfg.topk_group, cfg.norm_topk_prob, shared is not None,
+                             cfg.routed_scaling_factor, cfg.swiglu_limit)
+    cl = pyoracle.CpuLayer(ocfg, experts, shared, layer.router_w, layer.bias)
+    threads = pyoracle.cpu_threads()
+    # identity with the oracle on the sampled call
+    out0, idx0 = cl(h_list[0], threads)
+    oidx, _ = pyoracle.route(pyoracle.router_logits(h_list[0], layer.router_w), layer.bias, ocfg)
+    routing_equal = bool(np.array_equal(idx0, oidx))
+    checked = sorted(set(idx0.reshape(-1).tolist()))[:4]
+    weights_equal = all(
+        np.array_equal(pyoracle.cpu_decode(experts[3 * e + j]["trellis"], experts[3 * e + j]["in"],
+                                           experts[3 * e + j]["out"], experts[3 * e + j]["K"],
+                                           experts[3 * e + j]["cb"], threads),
+                       pyoracle.decode_inner(experts[3 * e + j]["trellis"], experts[3 * e + j]["in"],
+                                             experts[3 * e + j]["out"], experts[3 * e + j]["K"],
+                                             experts[3 * e + j]["cb"], threads))
+        for e in checked for j in range(3))
+    if not (routing_equal and weights_equal):
+        raise RuntimeError(f"CPU baseline differs from the oracle: routing {routing_equal}, "
+                           f"weights {weights_equal}")
+    vs_gpu = None
+    if gpu_out is not None:
+        a = out0.view(np.float16).astype(np.float64)
+        b = gpu_out.view(np.float16).astype(np.float64).reshape(a.shape)
+        vs_gpu = float(np.max(np.abs(a - b)) / np.sqrt(np.mean(b ** 2)))
+    cl(h_list[1 % len(h_list)], threads)  # second warm-up call
     times, nbytes = [], []
     t_start = time.time()
-    for i, h in enumerate(h_list):
+    i = 0
+    while i < 5 or (time.time() - t_start < budget_s and i < 1000):
+        h = h_list[i % len(h_list)]
         t0 = time.perf_counter()
-        _, idx, _ = pyoracle.moe_layer(ocfg, experts, shared, layer.router_w, layer.bias, h, threads)
+        _, idx = cl(h, threads)
         times.append(time.perf_counter() - t0)
-        distinct = set(idx.reshape(-1).tolist())
         nbytes.append(sum(layer.expert_trellis_bytes(e) if layer.experts[3 * e].trellis is not None
-                          else sum(words[3 * e + j].numel() * 2 for j in range(3)) for e in distinct))
-        if time.time() - t_start > budget_s and i >= 2:
-            break
+                          else sum(words[3 * e + j].numel() * 2 for j in range(3))
+                          for e in set(idx.reshape(-1).tolist())))
+        i += 1
     med = float(np.median(times))
     rows = h_list[0].shape[0]
-    # the same call on one thread, once (a bounded sample: about threads x the median)
     t0 = time.perf_counter()
-    pyoracle.moe_layer(ocfg, experts, shared, layer.router_w, layer.bias, h_list[0], 1)
+    cl(h_list[0], 1)
     t1 = time.perf_counter() - t0
-    return {"value": rows / med, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} calls of one GLM-5-shaped layer at B={rows} (distinct inputs), "
-                      f"median {med * 1e3:.0f} ms/call; oracle/exl3_oracle.c, {threads} threads; "
-                      f"one call on 1 thread: {t1 * 1e3:.0f} ms",
-            "value_1thread": rows / t1,
-            "trellis_GBps": float(np.median(nbytes)) / med / 1e9}
+    model, ncpu = cpu_model()
+    return {"value": round(rows / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} timed calls (after 2 warm-up calls) of one {cfg.hidden}-hidden, "
+                      f"{cfg.n_experts}-expert layer at B={rows} on {len(h_list)} distinct inputs, median "
+                      f"{med * 1e3:.2f} ms/call; oracle/cpu_layer.cpp (f32, -O3 AVX2/FMA/F16C), "
+                      f"{threads} threads; one call on 1 thread: {t1 * 1e3:.1f} ms",
+            "value_1thread": round(rows / t1, 3),
+            "trellis_GBps": round(float(np.median(nbytes)) / med / 1e9, 3),
+            "cpu_model": model, "host_logical_cpus": ncpu,
+            "routing_equal_oracle": routing_equal, "weights_equal_oracle": weights_equal,
+            "weights_checked": f"{3 * len(checked)} tensors of experts {checked}",
+            "max_err_rel_vs_gpu": vs_gpu}
 
 
 def main():
@@ -252,7 +312,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="glm5_moe_decode_b8",
                     help="the bench line's workload (default: the metric's B=8 decode); the "
-                         "others are measurement runs of configs[3] and configs[4]")
+                         "others are measurement runs of configs[0], [1], [3], [4] and of the "
+                         "B=8 layer at 1-4 rows")
     ap.add_argument("--steps", type=int, default=None, help="default 400 (prefill: 20)")
     ap.add_argument("--warmup", type=int, default=None, help="default 40 (prefill: 3)")
     ap.add_argument("--layers", type=int, default=None,
@@ -341,12 +402,14 @@ def main():
     gu_gbps = gu_bytes / (gu_ms * 1e-3) / 1e9
     dn_gbps = dn_bytes / (dn_ms * 1e-3) / 1e9
     routed_gbps = (gu_bytes + dn_bytes) / ((gu_ms + dn_ms) * 1e-3) / 1e9
-    distinct = (gu_bytes + dn_bytes) / 6815744.0
+    expert_bytes = (2 * H * cfg.inter * cfg.gate_up_K + cfg.inter * H * cfg.down_K) // 8
+    distinct = (gu_bytes + dn_bytes) / expert_bytes
 
     # f16 MFMA work of the routed gate/up launch: 2 flops per weight and routed pair
     gu_flops = 2.0 * 2 * H * cfg.inter * B * cfg.top_k
     gu_tflops = gu_flops / (gu_ms * 1e-3) / 1e12
-    shared = ("fp16 1024" if cfg.shared_K == 0 else f"K{cfg.shared_K} trellis {cfg.shared_inter}")
+    shared = ("none" if not cfg.shared_inter else
+              f"fp16 {cfg.shared_inter}" if cfg.shared_K == 0 else f"K{cfg.shared_K} trellis {cfg.shared_inter}")
     cbn = {0: "3inst", 1: "mcg", 2: "mul1"}
     metric = ("MoE-layer decode tokens/s + achieved HBM GB/s on trellis bytes, B=8, 1 MI355X"
               if args.workload == "glm5_moe_decode_b8" else
@@ -394,12 +457,14 @@ def main():
                             "frac": round(gu_tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
                             "algorithmic_flops_per_launch": gu_flops, "avg_launch_ms": round(gu_ms, 5),
                             "hbm_GBps": round(gu_gbps, 1), "hbm_frac": round(gu_gbps / HBM_PEAK_GBPS, 4)}
-    if args.workload != "glm5_moe_decode_b8":
-        args.no_cpu_baseline = True  # the CPU leg is sampled on the metric's workload only
+    if args.workload not in ("glm5_moe_decode_b8", "small_b1"):
+        args.no_cpu_baseline = True  # the CPU leg is sampled on configs[0] and configs[2]
     if not args.no_cpu_baseline:
-        layer, words, _ = layers[0]
+        layer, words, d0 = layers[0]
         h_list = [synth.activations(args.seed, f"bench.cpu.x{i}", B, H) for i in range(8)]
-        line["cpu_baseline"] = cpu_baseline(layer, words, h_list, args.cpu_seconds)
+        y0 = d0(torch.from_numpy(h_list[0].view(np.float16)).to(dev).view(B, 1, H))
+        line["cpu_baseline"] = cpu_baseline(layer, words, h_list, args.cpu_seconds,
+                                            y0.cpu().numpy().view(np.uint16))
     else:
         line["cpu_baseline"] = None
     for _, _, d in layers:

@@ -345,3 +345,78 @@ def hc_mix(block_out, post, comb, residual):
                     np.ascontiguousarray(comb, np.float64).reshape(-1),
                     np.ascontiguousarray(residual, np.uint16).reshape(-1), P, N, D, out.reshape(-1))
     return out
+
+
+# --- the f32 -O3 threaded CPU baseline (oracle/cpu_layer.cpp) -------------------------
+
+_CPU = None
+
+
+def cpu_lib():
+    """oracle/libcpulayer.so: bench.py's CPU baseline of the layer (measurement
+    infrastructure; weights and routing bit-identical to the oracle's)."""
+    global _CPU
+    if _CPU is None:
+        lib()  # the baseline links the oracle's routing and tables
+        path = os.path.join(_HERE, "libcpulayer.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"CPU baseline not built: {path} (run __graft_entry__.build())")
+        L = C.CDLL(path)
+        L.cpu_decode.argtypes = [u16p, C.c_int64, C.c_int64, C.c_int, C.c_int, u16p, C.c_int]
+        L.cpu_router_logits.argtypes = [u16p, C.c_int64, u16p, C.c_int, C.c_int, f64p, C.c_int]
+        L.cpu_moe_layer.argtypes = [C.POINTER(OrMoeCfg), C.POINTER(OrLinear), C.c_void_p, u16p,
+                                    f32p, u16p, C.c_int64, u16p, i32p, C.c_int]
+        _CPU = L
+    return _CPU
+
+
+def cpu_threads():
+    """Worker threads for the CPU baseline: the CPUs this process may run on, capped by
+    OMP_NUM_THREADS where the host sets it (a GPU box grants one GPU's share of its
+    cores that way)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(cap))) if cap and cap.isdigit() else n
+
+
+def cpu_decode(trellis, in_f, out_f, K, cb, threads=0):
+    w = np.zeros((in_f, out_f), np.uint16)
+    rc = cpu_lib().cpu_decode(np.ascontiguousarray(trellis, np.uint16).reshape(-1), in_f, out_f, K, cb, w,
+                              threads or cpu_threads())
+    if rc:
+        raise ValueError("cpu_decode: bad geometry")
+    return w
+
+
+def cpu_router_logits(h, router_w, threads=0):
+    h = np.ascontiguousarray(h, np.uint16)
+    E, H = router_w.shape
+    N = h.size // H
+    out = np.zeros((N, E), np.float64)
+    cpu_lib().cpu_router_logits(h.reshape(-1), N, np.ascontiguousarray(router_w, np.uint16).reshape(-1), E, H,
+                                out.reshape(-1), threads or cpu_threads())
+    return out
+
+
+class CpuLayer:
+    """A layer's tables for repeated cpu_moe_layer calls (the arrays stay referenced)."""
+
+    def __init__(self, cfg: OrMoeCfg, experts, shared, router_w, bias):
+        self.cfg = cfg
+        self.ex = LayerArrays(experts)
+        self.sh = LayerArrays(shared) if shared else None
+        self.router_w = np.ascontiguousarray(router_w, np.uint16).reshape(-1)
+        self.bias = np.ascontiguousarray(bias, np.float32)
+
+    def __call__(self, h, threads=0):
+        h = np.ascontiguousarray(h, np.uint16).reshape(-1, self.cfg.hidden)
+        N = h.shape[0]
+        out = np.zeros((N, self.cfg.hidden), np.uint16)
+        idx = np.zeros((N, self.cfg.top_k), np.int32)
+        rc = cpu_lib().cpu_moe_layer(C.byref(self.cfg), self.ex.table,
+                                     C.cast(self.sh.table, C.c_void_p) if self.sh else None, self.router_w,
+                                     self.bias, h.reshape(-1), N, out.reshape(-1), idx.reshape(-1),
+                                     threads or cpu_threads())
+        if rc:
+            raise ValueError("cpu_moe_layer failed")
+        return out, idx

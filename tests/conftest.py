@@ -14,8 +14,8 @@ def pytest_configure(config):
 
 
 def _ensure_oracle():
-    so = os.path.join(ROOT, "oracle", "liboracle.so")
-    if not os.path.exists(so):
+    so = [os.path.join(ROOT, "oracle", f) for f in ("liboracle.so", "libcpulayer.so")]
+    if not all(os.path.exists(f) for f in so):
         subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
 
 

@@ -340,6 +340,37 @@ def test_glm5_layer_b8_vs_oracle(oracle, dev):
     d.close()
 
 
+@pytest.fixture(scope="module")
+def glm5_verify_layer(dev):
+    layer, words = glm5_layer_on_device(dev, 61, "glm5v")
+    d = DeviceMoeLayer(layer, dev, words=words)
+    yield layer, words, d
+    d.close()
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 4])
+def test_glm5_layer_verify_rows_vs_oracle(oracle, dev, glm5_verify_layer, B):
+    # rows 1-4 at GLM-5 shape: decode and the multi-row verify / MTP regime
+    # (glm5_mtp.cpp:55: the draft block calls the MoE on 2-4 rows); against the oracle at
+    # the north-star bound, and the B-row call equal to B single-row calls bit for bit
+    layer, words, d = glm5_verify_layer
+    cfg = layer.cfg
+    h = synth.activations(61, f"glm5v.x{B}", B, cfg.hidden)
+    x = to_dev(h, dev, B, 1, cfg.hidden)
+    y = d(x)
+    _, ids = d.route(x)
+    oc = ocfg_of(oracle, cfg, True)
+    idx, w, flips = check_routing(oracle, oracle.router_logits(h, layer.router_w), layer.bias,
+                                  ids.cpu().numpy(), oc)
+    used = set(idx.reshape(-1).tolist())
+    want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used), oracle_shared(layer, words),
+                                   h, idx, w)
+    rel, cos = check_out(y, want)
+    for b in range(B):
+        assert torch.equal(d(x[b:b + 1].contiguous()), y[b:b + 1])
+    print(f"\nglm5 B={B}: distinct experts {len(used)}, max|err|/rms {rel:.3g}, cos {cos:.7f}, flips {flips}")
+
+
 def check_diag_bytes(dg, run_len, cfg, pass_rows, mat_min_rows=16):
     """MoeRowsDiag semantics (reference glm5_moe.cpp:265-287): runs in the staged window,
     and each run's expert bytes once per weight pass (passes of pass_rows rows), from the
