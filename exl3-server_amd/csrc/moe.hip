@@ -1519,6 +1519,39 @@ exl3_status exl3_moe_layer(exl3_moe_layer_t layer, const uint16_t *h, int64_t B,
 
 namespace {
 
+// MoeRowsDiag of one finished call (synchronises the stream).
+exl3_status collect_diag(exl3_moe_layer_t layer, const MoeArgs &a, const MoeLayout &m, hipStream_t st) {
+  std::lock_guard<std::mutex> lk(layer->mu);
+  EXL3_HIP(hipStreamSynchronize(st));
+  int32_t nr = 0;
+  EXL3_HIP(hipMemcpy(&nr, a.n_runs, 4, hipMemcpyDeviceToHost));
+  std::vector<int32_t> rl(nr), re(nr);
+  if (nr > 0) {
+    EXL3_HIP(hipMemcpy(rl.data(), a.run_len, 4 * (size_t)nr, hipMemcpyDeviceToHost));
+    EXL3_HIP(hipMemcpy(re.data(), a.run_expert, 4 * (size_t)nr, hipMemcpyDeviceToHost));
+  }
+  exl3_moe_diag &d = layer->diag;
+  d.calls += 1;
+  d.pairs += m.P;
+  d.runs += nr;
+  d.distinct_experts += nr;
+  // a run's weights are streamed once per pass: passes of pass_rows rows on the
+  // short-run kernels, of kLongRows rows on the long-run ones (glm5_moe.cpp:280-287
+  // counts trellis_path_info(tw, r).passes the same way); a run counts as staged by
+  // the handle's mat_min_rows/mat_max_rows window
+  const int prow = a.fold ? kLongRows : a.pass_rows;
+  const exl3_tuning &tn = layer->tuning;
+  for (int i = 0; i < nr; ++i) {
+    const int r = rl[i];
+    d.run_hist[r >= 64 ? 64 : r] += 1;
+    d.shared_bytes += layer->expert_bytes[re[i]];
+    d.streamed_bytes += layer->expert_bytes[re[i]] * ((r + prow - 1) / prow);
+    if (tn.mat_min_rows > 0 && r >= tn.mat_min_rows && (tn.mat_max_rows <= 0 || r <= tn.mat_max_rows))
+      d.staged_runs += 1;
+  }
+  return EXL3_OK;
+}
+
 // One layer call over N token rows with its workspace. instrumented: honour the
 // handle's timing and diagnostics (both synchronise the stream; the allocation-free
 // entry point skips them).
@@ -1635,36 +1668,7 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
     }
   }
 
-  if (instrumented && layer->diag_on) {
-    std::lock_guard<std::mutex> lk(layer->mu);
-    EXL3_HIP(hipStreamSynchronize(st));
-    int32_t nr = 0;
-    EXL3_HIP(hipMemcpy(&nr, a.n_runs, 4, hipMemcpyDeviceToHost));
-    std::vector<int32_t> rl(nr), re(nr);
-    if (nr > 0) {
-      EXL3_HIP(hipMemcpy(rl.data(), a.run_len, 4 * (size_t)nr, hipMemcpyDeviceToHost));
-      EXL3_HIP(hipMemcpy(re.data(), a.run_expert, 4 * (size_t)nr, hipMemcpyDeviceToHost));
-    }
-    exl3_moe_diag &d = layer->diag;
-    d.calls += 1;
-    d.pairs += m.P;
-    d.runs += nr;
-    d.distinct_experts += nr;
-    // a run's weights are streamed once per pass: passes of pass_rows rows on the
-    // short-run kernels, of kLongRows rows on the long-run ones (glm5_moe.cpp:280-287
-    // counts trellis_path_info(tw, r).passes the same way); a run counts as staged by
-    // the handle's mat_min_rows/mat_max_rows window
-    const int prow = a.fold ? kLongRows : a.pass_rows;
-    const exl3_tuning &tn = layer->tuning;
-    for (int i = 0; i < nr; ++i) {
-      const int r = rl[i];
-      d.run_hist[r >= 64 ? 64 : r] += 1;
-      d.shared_bytes += layer->expert_bytes[re[i]];
-      d.streamed_bytes += layer->expert_bytes[re[i]] * ((r + prow - 1) / prow);
-      if (tn.mat_min_rows > 0 && r >= tn.mat_min_rows && (tn.mat_max_rows <= 0 || r <= tn.mat_max_rows))
-        d.staged_runs += 1;
-    }
-  }
+  if (instrumented && layer->diag_on) return collect_diag(layer, a, m, st);
   return EXL3_OK;
 }
 
