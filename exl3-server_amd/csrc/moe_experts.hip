@@ -312,41 +312,44 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int np = cb * kWaves + wave;
   const bool active = np < n_np;  // idle waves still stage rows and meet the barriers
   constexpr bool kDup = dup_cb(CB);
-  const int slice_k = kStepTiles * ss * 16;
-  const int xs_stride = staged_row_words(k_tiles, kDup);
+  const int part = long_part_steps(k_tiles, kDup), n_parts = ss / part;
+  const int part_k = kStepTiles * part * 16;
+  const int xs_stride = long_row_words(k_tiles, kDup);
   uint32_t *xs = smem;
   u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * slot_chunks(K);
 
-  const int q_row = slice_k / 8;  // 16-byte chunks of xrot per row
+  const int q_row = part_k / 8;  // 16-byte chunks of xrot per row and part (a power of two)
+  const int q_lg = __builtin_ctz(q_row);
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
-    f32x4 acc[kLongBlocks][2];
+    f32x4 acc[kLongBlocks][2], D[kLongBlocks][2];
     for (int sl = 0; sl < n_sl; ++sl) {
-      // the slice of the pass's rows, already rotated by k_moe_rotate (x_rot rows of
-      // this projection, in the staged k order)
-      const int items = nr * q_row;
-      for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatch) {
-        uint4 c[kStageBatch];
+      for (int pt = 0; pt < n_parts; ++pt) {
+        // the part of the pass's rows, already rotated by k_moe_rotate (x_rot rows of
+        // this projection, in the staged k order)
+        const int k0 = (sl * n_parts + pt) * part_k;
+        const int items = nr * q_row;
+        for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatch) {
+          uint4 c[kStageBatch];
 #pragma unroll
-        for (int q = 0; q < kStageBatch; ++q) {
-          const int i = min(i0 + q * kLongThreads, items - 1);
-          c[q] = reinterpret_cast<const uint4 *>(
-              a.xrot + ((int64_t)(ri.off + p0 + i / q_row) * 2 + proj) * a.H + sl * slice_k)[i % q_row];
-        }
+          for (int q = 0; q < kStageBatch; ++q) {
+            const int i = min(i0 + q * kLongThreads, items - 1);
+            c[q] = reinterpret_cast<const uint4 *>(
+                a.xrot + ((int64_t)(ri.off + p0 + (i >> q_lg)) * 2 + proj) * a.H + k0)[i & (q_row - 1)];
+          }
 #pragma unroll
-        for (int q = 0; q < kStageBatch; ++q) {
-          const int i = i0 + q * kLongThreads;
-          if (i < items) stage_chunk<kDup>(xs + (i / q_row) * xs_stride, i % q_row, c[q]);
+          for (int q = 0; q < kStageBatch; ++q) {
+            const int i = i0 + q * kLongThreads;
+            if (i < items) stage_chunk<kDup>(xs + (i >> q_lg) * xs_stride, i & (q_row - 1), c[q]);
+          }
         }
+        __syncthreads();
+        if (active)
+          qmv_slice_rb<K, CB, PD, kLongBlocks>(base, k_tiles, out / 16, k0 / 16, np, part, xs, xs_stride,
+                                               nr, slot, D, pt == 0);
+        __syncthreads();
       }
-      __syncthreads();
-      if (active) {
-        f32x4 D[kLongBlocks][2];
-        qmv_slice_rb<K, CB, PD, kLongBlocks>(base, k_tiles, out / 16, sl * kStepTiles * ss, np, ss,
-                                             xs, xs_stride, nr, slot, D);
-        fold_partials<kLongBlocks>(acc, D, sl == 0);
-      }
-      __syncthreads();
+      if (active) fold_partials<kLongBlocks>(acc, D, sl == 0);
     }
     if (active) {
       const int col = np * 32;
@@ -385,39 +388,42 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int np = cb * kWaves + wave;
   const bool active = np < n_np;
   constexpr bool kDup = dup_cb(CB);
-  const int slice_k = kStepTiles * ss * 16;
-  const int xs_stride = staged_row_words(k_tiles, kDup);
-  const int q_row = slice_k / 8;  // 16-byte chunks of act per row
+  const int part = long_part_steps(k_tiles, kDup), n_parts = ss / part;
+  const int part_k = kStepTiles * part * 16;
+  const int xs_stride = long_row_words(k_tiles, kDup);
+  const int q_row = part_k / 8;  // 16-byte chunks of act per row and part (a power of two)
+  const int q_lg = __builtin_ctz(q_row);
   uint32_t *xs = smem;
   u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * slot_chunks(K);
 
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
-    f32x4 acc[kLongBlocks][2];
+    f32x4 acc[kLongBlocks][2], D[kLongBlocks][2];
     for (int sl = 0; sl < n_sl; ++sl) {
-      const int items = nr * q_row;  // 16-byte chunks of the slice's rows
-      for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatch) {
-        uint4 c[kStageBatch];
+      for (int pt = 0; pt < n_parts; ++pt) {
+        const int k0 = (sl * n_parts + pt) * part_k;
+        const int items = nr * q_row;  // 16-byte chunks of the part's rows
+        for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatch) {
+          uint4 c[kStageBatch];
 #pragma unroll
-        for (int q = 0; q < kStageBatch; ++q) {
-          const int i = min(i0 + q * kLongThreads, items - 1);
-          c[q] = reinterpret_cast<const uint4 *>(a.act + (int64_t)(ri.off + p0 + i / q_row) * a.Imax +
-                                                 sl * slice_k)[i % q_row];
-        }
+          for (int q = 0; q < kStageBatch; ++q) {
+            const int i = min(i0 + q * kLongThreads, items - 1);
+            c[q] = reinterpret_cast<const uint4 *>(a.act + (int64_t)(ri.off + p0 + (i >> q_lg)) * a.Imax +
+                                                   k0)[i & (q_row - 1)];
+          }
 #pragma unroll
-        for (int q = 0; q < kStageBatch; ++q) {
-          const int i = i0 + q * kLongThreads;
-          if (i < items) stage_chunk<kDup>(xs + (i / q_row) * xs_stride, i % q_row, c[q]);
+          for (int q = 0; q < kStageBatch; ++q) {
+            const int i = i0 + q * kLongThreads;
+            if (i < items) stage_chunk<kDup>(xs + (i >> q_lg) * xs_stride, i & (q_row - 1), c[q]);
+          }
         }
+        __syncthreads();
+        if (active)
+          qmv_slice_rb<K, CB, PD, kLongBlocks>(tb.tr[2], k_tiles, a.H / 16, k0 / 16, np, part, xs, xs_stride,
+                                               nr, slot, D, pt == 0);
+        __syncthreads();
       }
-      __syncthreads();
-      if (active) {
-        f32x4 D[kLongBlocks][2];
-        qmv_slice_rb<K, CB, PD, kLongBlocks>(tb.tr[2], k_tiles, a.H / 16, sl * kStepTiles * ss, np,
-                                             ss, xs, xs_stride, nr, slot, D);
-        fold_partials<kLongBlocks>(acc, D, sl == 0);
-      }
-      __syncthreads();
+      if (active) fold_partials<kLongBlocks>(acc, D, sl == 0);
     }
     if (active) {
       const int col = np * 32;
@@ -550,6 +556,9 @@ namespace exl3h {
 static size_t expert_lds(int in, int pass_rows, int waves, int K, int cb) {
   return (size_t)pass_rows * staged_row_words(in / 16, dup_cb(cb)) * 4 + (size_t)waves * slot_chunks(K) * 16;
 }
+static size_t long_lds(int in, int K, int cb) {
+  return (size_t)kLongRows * long_row_words(in / 16, dup_cb(cb)) * 4 + (size_t)(kLongThreads / 64) * slot_chunks(K) * 16;
+}
 
 int moe_slices(int in) { return n_slices(in / 16); }
 
@@ -580,7 +589,7 @@ static exl3_status moe_go(int which, dim3 blocks, hipStream_t st, const MoeArgs 
   const int in = which == 0 ? a.H : (shared_mode ? a.SI : a.I);
   if (a.fold) {
     if constexpr (PD <= 2) {  // long-run kernels keep at most 2 steps in flight (VGPRs)
-      const size_t lds = expert_lds(in, kLongRows, kLongThreads / 64, K, CB);
+      const size_t lds = long_lds(in, K, CB);
       static KernelAttr set_gu, set_dn;
       return which == 0 ? launch_kernel(k_moe_gate_up_long<K, CB, PD>, blocks, kLongThreads, lds, st,
                                         a, shared_mode, dense_blocks, set_gu)
@@ -633,7 +642,7 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
   const int out = which == 0 ? (shared_mode ? a.SI : a.I) : a.H;
   const int n_sl = n_slices(in / 16);
   const int waves = a.fold ? kLongThreads / 64 : kGuThreads / 64;
-  if (expert_lds(in, a.fold ? kLongRows : a.pass_rows, waves, K, cb) > 128 * 1024)
+  if ((a.fold ? long_lds(in, K, cb) : expert_lds(in, a.pass_rows, waves, K, cb)) > 128 * 1024)
     return fail(EXL3_ERR_UNSUPPORTED, "expert kernel LDS above 128 KB");
   const int items = which == 0 ? a.gu_items : a.dn_items;
   if (!a.fold && items < 1) return fail(EXL3_ERR_INVALID, "column blocks per expert workgroup below 1");

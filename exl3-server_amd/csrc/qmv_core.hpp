@@ -85,6 +85,15 @@ __host__ __device__ constexpr int slice_words(int k_tiles, bool dup) {
 __host__ __device__ constexpr int staged_row_words(int k_tiles, bool dup) {
   return slice_words(k_tiles, dup) + 4;
 }
+// The long-run kernels stage a slice of duplicated rows in parts of at most 4 wave
+// steps (a part of 48 rows is ~50 KB of LDS, so that two 8-wave workgroups share a CU;
+// a whole slice of plain rows is that size already).
+__host__ __device__ constexpr int long_part_steps(int k_tiles, bool dup) {
+  return !dup || slice_steps(k_tiles) < 4 ? slice_steps(k_tiles) : 4;
+}
+__host__ __device__ constexpr int long_row_words(int k_tiles, bool dup) {
+  return kStepTiles * long_part_steps(k_tiles, dup) * tile_words(dup) + 4;
+}
 // 16-byte ring-word chunks of one wave's LDS slot: one wave step's 16K chunks, and at
 // least one per lane (every lane stores its first chunk register, K < 4 included).
 __host__ __device__ constexpr int slot_chunks(int K) { return 16 * K > 64 ? 16 * K : 64; }
@@ -403,11 +412,13 @@ __device__ __forceinline__ void mfma_step_rb(const uint32_t (&W)[K + 1], const u
 
 // qmv_slice over up to 16 * RB staged token rows: xs = the first staged row (row
 // stride xs_stride words), nrows = rows staged (>= 1); rows past nrows read the last
-// row and are never stored. D[b] = the slice partials of rows 16b .. 16b + 15.
+// row and are never stored. D[b] = the slice partials of rows 16b .. 16b + 15, from
+// zero, or (zero = false) continuing the accumulation already in D: a slice run as
+// consecutive parts adds every step into its accumulator in the same order as one call.
 template <int K, int CB, int PD, int RB>
 __device__ __forceinline__ void qmv_slice_rb(const uint32_t *base, int k_tiles, int tiles_n, int kt0,
                                              int np, int nsteps, const uint32_t *xs, int xs_stride,
-                                             int nrows, u32x4 *slot, f32x4 (&D)[RB][2]) {
+                                             int nrows, u32x4 *slot, f32x4 (&D)[RB][2], bool zero = true) {
   constexpr int kTw = tile_words(dup_cb(CB));
   const StepLane sl = step_lane();
   const int lane = threadIdx.x & 63;
@@ -430,10 +441,12 @@ __device__ __forceinline__ void qmv_slice_rb(const uint32_t *base, int k_tiles, 
   StepLoads<K> L[PD];
 #pragma unroll
   for (int b = 0; b < PD; ++b) step_load<K>(rsrc, vo0, vo1, so0 + b * step_bytes, L[b]);
+  if (zero) {
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    D[r][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    D[r][1] = D[r][0];
+    for (int r = 0; r < RB; ++r) {
+      D[r][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      D[r][1] = D[r][0];
+    }
   }
   int s0 = 0;
   for (; s0 < nsteps - PD; s0 += PD) {
