@@ -67,6 +67,8 @@ WORKLOADS = {
                                                "down K5 mul1, shared K6 mcg, 8 hot experts"),
     "small_b1": ("small", 1, "configs[0]: small EXL3 MoE layer (hidden 512, 16 experts, top-2, K4 mcg), "
                              "batch-1 decode"),
+    "glm5_moe_block_b8": ("block", 8, "the MLP sub-block of the B=8 layer: hyper-connection prepare (4 streams), "
+                                      "RMSNorm, the MoE, hyper-connection mix"),
     "trellis_linear": ("linear", 1, "configs[1]: one trellis linear at rows=1 (in 4096), K=1..8 x 3 codebooks"),
 }
 
@@ -121,6 +123,16 @@ def bench_linear(args):
     steps = args.steps if args.steps is not None else 400
     warmup = args.warmup if args.warmup is not None else 40
     ms, gbps = run(4096, 24576, 4, steps, warmup)
+    # the reference's headline tensor classes (tests/glm5_gemv_nt_test.cpp:147-171) at rows = 1
+    classes = {}
+    for name, (i_f, o_f, K, cb) in (("lm_head 4096x154880 K6 mcg", (4096, 154880, 6, 1)),
+                                    ("kda qkv 4096x24576 K4 mul1", (4096, 24576, 4, 2)),
+                                    ("mla o_proj 16384x4096 K6 mcg", (16384, 4096, 6, 1)),
+                                    ("kda o_proj 8192x4096 K4 mcg", (8192, 4096, 4, 1)),
+                                    ("expert gate 4096x2048 K3 mul1", (4096, 2048, 3, 2)),
+                                    ("expert gate 4096x2048 K2 mul1", (4096, 2048, 2, 2))):
+        kms, kg = run(i_f, o_f, K, max(50, steps // 4), max(5, warmup // 4), cb)
+        classes[name] = {"ms": round(kms, 5), "GBps": round(kg, 1)}
     sweep = {}
     for cb, name in ((0, "3inst"), (1, "mcg"), (2, "mul1")):
         for K in range(1, 9):
@@ -136,13 +148,83 @@ def bench_linear(args):
         "roofline": {"kernel": "exl3_trellis_linear (QMV with the input Hadamard, finalize)", "bound": "hbm",
                      "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
-        "sweep_4096x4096": sweep, "cpu_baseline": None,
+        "sweep_4096x4096": sweep, "classes_rows1": classes, "cpu_baseline": None,
     }
     print(json.dumps(line))
 HOT_BIAS = 0.23  # bias tilt that sends about a quarter of the selections to 8 hot experts
 
 
 VALU_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_glm5_b8_valu.md")
+
+
+def bench_block(args):
+    """exl3_moe_block at B=8 on the GLM-5 layer (glm5_forward.cpp:434-438): g5_hc_prepare of
+    4 residual streams (RMS over 16384 values, 24 projections, 20 Sinkhorn iterations) with
+    the RMSNorm fused, the MoE layer, and g5_hc_mix fused into its combine; seeded synthetic
+    hyper-connection weights. The same layer instances' plain exl3_moe_layer calls are
+    timed in the same run, so hc_overhead_ms is what the steps either side cost."""
+    import numpy as np
+    import torch
+    from exl3_amd import synth
+    from exl3_amd.hc import DeviceHcSite, moe_block
+
+    steps = args.steps if args.steps is not None else 400
+    warmup = args.warmup if args.warmup is not None else 40
+    n_layers = args.layers if args.layers is not None else 8
+    dev = torch.device("cuda:0")
+    cfg, layers = build_layers(n_layers, args.seed, dev, "glm5")
+    H, B, NS = cfg.hidden, 8, 4
+    rng = np.random.default_rng(args.seed)
+    W = (2 + NS) * NS
+    sites, norms, streams, outs, wss, xs, ys = [], [], [], [], [], [], []
+    for li, (_, _, d) in enumerate(layers):
+        fn = (rng.normal(size=(W, NS * H)) / np.sqrt(NS * H)).astype(np.float32)
+        base = (rng.normal(size=W) * 0.5).astype(np.float32)
+        sites.append(DeviceHcSite.from_numpy(fn, base, np.ones(3, np.float32), NS, 20, 1e-6, dev))
+        norms.append(torch.from_numpy(rng.normal(1.0, 0.05, H).astype(np.float16)).to(dev))
+        streams.append(torch.from_numpy(rng.normal(size=(B, NS, H)).astype(np.float16)).to(dev))
+        outs.append(torch.empty_like(streams[-1]))
+        wss.append(torch.empty(max(256, d.workspace_bytes(B) * 2 + (64 << 20)), dtype=torch.uint8, device=dev))
+        xs.append(streams[-1][:, 0].contiguous().view(B, 1, H))
+        ys.append(torch.empty_like(xs[-1]))
+
+    def block(i):
+        li = i % n_layers
+        moe_block(layers[li][2], sites[li], norms[li], 1e-5, streams[li], out=outs[li], ws=wss[li])
+
+    def layer(i):
+        li = i % n_layers
+        layers[li][2](xs[li], out=ys[li], ws=wss[li])
+
+    def timed(fn):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for i in range(steps):
+            fn(i)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) * 1e3 / steps
+
+    block_ms = timed(block)
+    layer_ms = timed(layer)
+    block_ms2 = timed(block)
+    ms = min(block_ms, block_ms2)
+    line = {
+        "metric": "MoE MLP sub-block tokens/s (hc prepare + RMSNorm + MoE + hc mix), B=8, 1 MI355X",
+        "value": round(B / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "glm5_moe_block_b8", "batch": B, "hidden": H, "hc_mult": NS, "sinkhorn_iters": 20,
+                   "experts": cfg.n_experts, "top_k": cfg.top_k, "layer_instances": n_layers,
+                   "parallelism": "none (one GPU)"},
+        "layer_only_ms_per_step": round(layer_ms, 5),
+        "hc_overhead_ms": round(ms - layer_ms, 5),
+        "roofline": None, "cpu_baseline": None,
+    }
+    for _, _, d in layers:
+        d.close()
+    print(json.dumps(line))
 
 
 def profiled_valu_busy(kernel):
@@ -338,6 +420,9 @@ def main():
     kind, B, _ = WORKLOADS[args.workload]
     if kind == "linear":
         bench_linear(args)
+        return
+    if kind == "block":
+        bench_block(args)
         return
     prefill = kind == "prefill"
     args.steps = args.steps if args.steps is not None else (20 if prefill else 400)

@@ -33,7 +33,7 @@ namespace {
 
 constexpr int kHcMaxN = 4;                       // streams (W <= 24), as the reference's fused path
 constexpr int kHcMaxW = (2 + kHcMaxN) * kHcMaxN;
-constexpr int kHcChunk = 256;                    // elements of the N*D axis per workgroup
+constexpr int kHcChunk = 64;                     // elements of the N*D axis per workgroup
 constexpr int kHcRows = 8;                       // positions per projection workgroup
 constexpr int kHcVals = kHcMaxW + 1;             // per chunk: W projections, then the sum of squares
 
@@ -49,44 +49,53 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ float h2f(uint16_t v) { return (float)bitcast<f16>(v); }
 
+// Thread (j, r): projection j < W of position p0 + r (r < kHcRows), the dot product of
+// the workgroup's chunk of the N*D axis with fn row j, in k order; threads past the
+// projections: the chunk's sum of squares of position p0 + r. All of a thread's loads are
+// in flight at once; no cross-lane reduction.
+constexpr int kHcProjThreads = (kHcMaxW + 1) * kHcRows;  // 200
+
 __global__ __launch_bounds__(256) void k_hc_proj(const uint16_t *__restrict__ streams, int64_t P, int ND, int W,
                                                  const float *__restrict__ fn, float *__restrict__ part) {
   const int chunk = blockIdx.x, n_chunks = gridDim.x;
-  const int64_t p0 = (int64_t)blockIdx.y * kHcRows;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int k0 = chunk * kHcChunk + 4 * lane;  // this lane's 4 elements
-  // projections j = wave, wave + 4, ...: their fn slices, kept for every position
-  constexpr int kPer = kHcMaxW / 4;
-  float4 f[kPer];
+  const int t = threadIdx.x;
+  if (t >= kHcProjThreads) return;
+  const bool sq = t >= kHcMaxW * kHcRows;
+  const int j = sq ? kHcMaxW : t / kHcRows, r = t % kHcRows;
+  const int64_t p = (int64_t)blockIdx.y * kHcRows + r;
+  if (p >= P || (!sq && j >= W)) return;
+  const int k0 = chunk * kHcChunk;
+  const uint16_t *s = streams + p * ND + k0;
+  const float *f = fn + (int64_t)(sq ? 0 : j) * ND + k0;
+  // the chunk's 16 groups of 4 elements, every load in flight at once
+  constexpr int kGroups = kHcChunk / 4;
+  uint2 sv[kGroups];
+  float4 fv[kGroups];
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int j = wave + 4 * q;
-    f[q] = j < W ? *reinterpret_cast<const float4 *>(fn + (int64_t)j * ND + k0) : float4{0, 0, 0, 0};
+  for (int q = 0; q < kGroups; ++q) {
+    sv[q] = *reinterpret_cast<const uint2 *>(s + 4 * q);
+    if (!sq) fv[q] = *reinterpret_cast<const float4 *>(f + 4 * q);
   }
-  for (int r = 0; r < kHcRows && p0 + r < P; ++r) {
-    const int64_t p = p0 + r;
-    const uint2 sv = *reinterpret_cast<const uint2 *>(streams + p * ND + k0);
-    const float s0 = h2f(sv.x & 0xffff), s1 = h2f(sv.x >> 16), s2 = h2f(sv.y & 0xffff), s3 = h2f(sv.y >> 16);
-    float *out = part + (p * n_chunks + chunk) * kHcVals;
+  float acc = 0.0f;
+  {
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int j = wave + 4 * q;
-      float d = s0 * f[q].x;
-      d = fmaf(s1, f[q].y, d);
-      d = fmaf(s2, f[q].z, d);
-      d = fmaf(s3, f[q].w, d);
-      d = wave_sum(d);
-      if (j < W && lane == 0) out[j] = d;
-    }
-    if (wave == 0) {
-      float ss = s0 * s0;
-      ss = fmaf(s1, s1, ss);
-      ss = fmaf(s2, s2, ss);
-      ss = fmaf(s3, s3, ss);
-      ss = wave_sum(ss);
-      if (lane == 0) out[kHcMaxW] = ss;
+    for (int q = 0; q < kGroups; ++q) {
+      const float s0 = h2f(sv[q].x & 0xffff), s1 = h2f(sv[q].x >> 16), s2 = h2f(sv[q].y & 0xffff),
+                  s3 = h2f(sv[q].y >> 16);
+      if (sq) {
+        acc = fmaf(s0, s0, acc);
+        acc = fmaf(s1, s1, acc);
+        acc = fmaf(s2, s2, acc);
+        acc = fmaf(s3, s3, acc);
+      } else {
+        acc = fmaf(s0, fv[q].x, acc);
+        acc = fmaf(s1, fv[q].y, acc);
+        acc = fmaf(s2, fv[q].z, acc);
+        acc = fmaf(s3, fv[q].w, acc);
+      }
     }
   }
+  part[(p * n_chunks + chunk) * kHcVals + j] = acc;
 }
 
 // Sum of one value over a workgroup of 4 waves, the waves' sums added in wave order.
@@ -100,30 +109,38 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
   return t;
 }
 
-// y = f16(f16(x * r) * w) for this thread's elements (x already f16 values in f32).
-template <int PER>
-__device__ __forceinline__ void rms_apply(const float (&x)[PER], int D, float eps, const uint16_t *w, uint16_t *y,
-                                          float *red) {
+constexpr int kHcMaxD = 8192;
+constexpr int kHcPairs = kHcMaxD / 512;  // element pairs per thread at the largest hidden size
+
+// This thread's pairs of a row: d = 2 * (threadIdx.x + 256 * i).
+__device__ __forceinline__ int pair_d(int i) { return 2 * ((int)threadIdx.x + 256 * i); }
+
+// y = f16(f16(x * r) * w) on this thread's pairs (x0/x1: the pairs' f16 values in f32),
+// r = rsqrt(mean(x^2) + eps) of the row: the thread's squares summed in pair order, then
+// the workgroup's sum. The norm weights' loads are issued first.
+__device__ __forceinline__ void rms_pairs(const float (&x0)[kHcPairs], const float (&x1)[kHcPairs], int D,
+                                          float eps, const uint16_t *w, uint16_t *y, float *red) {
+  uint32_t wv[kHcPairs];
+#pragma unroll
+  for (int i = 0; i < kHcPairs; ++i)
+    wv[i] = pair_d(i) < D ? *reinterpret_cast<const uint32_t *>(w + pair_d(i)) : 0u;
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = threadIdx.x + 256 * i;
-    if (d < D) ss = fmaf(x[i], x[i], ss);
-  }
+  for (int i = 0; i < kHcPairs; ++i)
+    if (pair_d(i) < D) {
+      ss = fmaf(x0[i], x0[i], ss);
+      ss = fmaf(x1[i], x1[i], ss);
+    }
   const float total = block_sum(ss, red);
   const float r = 1.0f / sqrtf(total / (float)D + eps);
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = threadIdx.x + 256 * i;
-    if (d < D) {
-      const float n = (float)to_f16(x[i] * r);
-      y[d] = f32_to_f16(n * h2f(w[d]));
+  for (int i = 0; i < kHcPairs; ++i)
+    if (pair_d(i) < D) {
+      const float n0 = (float)to_f16(x0[i] * r), n1 = (float)to_f16(x1[i] * r);
+      *reinterpret_cast<uint32_t *>(y + pair_d(i)) =
+          (uint32_t)f32_to_f16(n0 * h2f(wv[i] & 0xffff)) | ((uint32_t)f32_to_f16(n1 * h2f(wv[i] >> 16)) << 16);
     }
-  }
 }
-
-constexpr int kHcMaxD = 8192;
-constexpr int kHcPer = kHcMaxD / 256;
 
 __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict__ streams, int N, int D, int W,
                                                      int n_chunks, const float *__restrict__ part,
@@ -132,96 +149,138 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
                                                      float norm_eps, uint16_t *__restrict__ out,
                                                      float *__restrict__ post_out, float *__restrict__ comb_out) {
   __shared__ float vals[kHcVals];
+  __shared__ float grp[8][32];
   __shared__ float pre[kHcMaxN];
   __shared__ float red[4];
   const int64_t p = blockIdx.x;
   const int64_t ND = (int64_t)N * D;
   const int t = threadIdx.x;
-  // the chunk partials in chunk order
+  // the row's stream pairs, in flight while the projections are finished
+  const uint16_t *srow = streams + p * ND;
+  uint32_t sp[kHcMaxN][kHcPairs];
+#pragma unroll
+  for (int n = 0; n < kHcMaxN; ++n)
+#pragma unroll
+    for (int i = 0; i < kHcPairs; ++i)
+      sp[n][i] = n < N && pair_d(i) < D ? *reinterpret_cast<const uint32_t *>(srow + (int64_t)n * D + pair_d(i))
+                                        : 0u;
+  // the chunk partials: thread (g, j) sums value j over chunks g, g + 8, ... in order
+  // (their loads in flight together), then value j is the sum of the 8 group sums in
+  // group order
+  {
+    const int j = t & 31, g = t >> 5;
+    float acc = 0.0f;
+    if (j < W || j == kHcMaxW) {
+      const float *pp = part + p * n_chunks * kHcVals + j;
+      for (int c0 = g; c0 < n_chunks; c0 += 8 * 16) {
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = pp[(int64_t)min(c0 + 8 * q, n_chunks - 1) * kHcVals];
+#pragma unroll
+        for (int q = 0; q < 16; ++q)
+          if (c0 + 8 * q < n_chunks) acc += v[q];
+      }
+    }
+    grp[g][j] = acc;
+  }
+  __syncthreads();
   if (t < W || t == kHcMaxW) {
-    const float *pp = part + p * n_chunks * kHcVals + t;
-    float acc = pp[0];
-    for (int c = 1; c < n_chunks; ++c) acc += pp[(int64_t)c * kHcVals];
+    float acc = grp[0][t];
+#pragma unroll
+    for (int g = 1; g < 8; ++g) acc += grp[g][t];
     vals[t] = acc;
   }
   __syncthreads();
-  if (t == 0) {
+  if (t < 64) {
+    // wave 0, one lane per value: lane l < N*N holds comb entry (l / N, l % N); row and
+    // column reductions gather the N entries by shuffles, in index order
     const float rms = 1.0f / sqrtf(vals[kHcMaxW] / (float)ND + eps);
-    float w[kHcMaxW];
-    for (int j = 0; j < W; ++j) w[j] = vals[j] * rms;
-    for (int n = 0; n < N; ++n) {
-      pre[n] = 1.0f / (1.0f + expf(-(w[n] * scale[0] + base[n]))) + eps;
-      post_out[p * N + n] = 2.0f * (1.0f / (1.0f + expf(-(w[N + n] * scale[1] + base[N + n]))));
+    const int lane = t;
+    if (lane < N) {
+      const float wp = vals[lane] * rms, wq = vals[N + lane] * rms;
+      pre[lane] = 1.0f / (1.0f + expf(-(wp * scale[0] + base[lane]))) + eps;
+      post_out[p * N + lane] = 2.0f * (1.0f / (1.0f + expf(-(wq * scale[1] + base[N + lane]))));
     }
-    float c[kHcMaxN * kHcMaxN];
-    for (int i = 0; i < N; ++i) {
-      float m = -INFINITY;
-      for (int j = 0; j < N; ++j) {
-        const float z = w[2 * N + i * N + j] * scale[2] + base[2 * N + i * N + j];
-        c[i * N + j] = z;
-        m = fmaxf(m, z);
-      }
-      float s = 0.0f;
-      for (int j = 0; j < N; ++j) {
-        c[i * N + j] = expf(c[i * N + j] - m);
-        s += c[i * N + j];
-      }
-      for (int j = 0; j < N; ++j) c[i * N + j] = c[i * N + j] / s + eps;
-    }
-    for (int j = 0; j < N; ++j) {
-      float cs = 0.0f;
-      for (int i = 0; i < N; ++i) cs += c[i * N + j];
-      for (int i = 0; i < N; ++i) c[i * N + j] = c[i * N + j] / (cs + eps);
-    }
+    const int NN = N * N;
+    const bool live = lane < NN;
+    const int ci = live ? lane / N : 0, cj = live ? lane % N : 0;
+    const float z = live ? vals[2 * N + lane] * rms * scale[2] + base[2 * N + lane] : 0.0f;
+    auto row_sum = [&](float v) {
+      float o[kHcMaxN];
+#pragma unroll
+      for (int k = 0; k < kHcMaxN; ++k) o[k] = __shfl(v, ci * N + min(k, N - 1), 64);
+      float s = o[0];
+#pragma unroll
+      for (int k = 1; k < kHcMaxN; ++k)
+        if (k < N) s += o[k];
+      return s;
+    };
+    auto col_sum = [&](float v) {
+      float o[kHcMaxN];
+#pragma unroll
+      for (int k = 0; k < kHcMaxN; ++k) o[k] = __shfl(v, min(k, N - 1) * N + cj, 64);
+      float s = o[0];
+#pragma unroll
+      for (int k = 1; k < kHcMaxN; ++k)
+        if (k < N) s += o[k];
+      return s;
+    };
+    // softmax over the last axis (j), then + eps
+    float o[kHcMaxN];
+#pragma unroll
+    for (int k = 0; k < kHcMaxN; ++k) o[k] = __shfl(z, ci * N + min(k, N - 1), 64);
+    float m = o[0];
+#pragma unroll
+    for (int k = 1; k < kHcMaxN; ++k)
+      if (k < N) m = fmaxf(m, o[k]);
+    float c = expf(z - m);
+    c = c / row_sum(c) + eps;
+    // Sinkhorn: columns, then (iters - 1) x (rows, columns)
+    c = c / (col_sum(c) + eps);
     for (int it = 0; it < iters - 1; ++it) {
-      for (int i = 0; i < N; ++i) {
-        float rs = 0.0f;
-        for (int j = 0; j < N; ++j) rs += c[i * N + j];
-        for (int j = 0; j < N; ++j) c[i * N + j] = c[i * N + j] / (rs + eps);
-      }
-      for (int j = 0; j < N; ++j) {
-        float cs = 0.0f;
-        for (int i = 0; i < N; ++i) cs += c[i * N + j];
-        for (int i = 0; i < N; ++i) c[i * N + j] = c[i * N + j] / (cs + eps);
-      }
+      c = c / (row_sum(c) + eps);
+      c = c / (col_sum(c) + eps);
     }
-    for (int k = 0; k < N * N; ++k) comb_out[p * N * N + k] = c[k];
+    if (live) comb_out[p * NN + lane] = c;
   }
   __syncthreads();
   // collapsed = sum_n pre[n] * streams[n], in f16
-  const uint16_t *s = streams + p * ND;
-  float x[kHcPer];
+  float x0[kHcPairs], x1[kHcPairs];
 #pragma unroll
-  for (int i = 0; i < kHcPer; ++i) {
-    const int d = t + 256 * i;
-    float a = 0.0f;
-    if (d < D) {
-      for (int n = 0; n < N; ++n) a = fmaf(pre[n], h2f(s[(int64_t)n * D + d]), a);
-    }
-    x[i] = (float)to_f16(a);
+  for (int i = 0; i < kHcPairs; ++i) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int n = 0; n < kHcMaxN; ++n)
+      if (n < N) {
+        a0 = fmaf(pre[n], h2f(sp[n][i] & 0xffff), a0);
+        a1 = fmaf(pre[n], h2f(sp[n][i] >> 16), a1);
+      }
+    x0[i] = (float)to_f16(a0);
+    x1[i] = (float)to_f16(a1);
   }
   if (!norm_w) {
 #pragma unroll
-    for (int i = 0; i < kHcPer; ++i) {
-      const int d = t + 256 * i;
-      if (d < D) out[p * D + d] = f32_to_f16(x[i]);
-    }
+    for (int i = 0; i < kHcPairs; ++i)
+      if (pair_d(i) < D)
+        *reinterpret_cast<uint32_t *>(out + p * D + pair_d(i)) =
+            (uint32_t)f32_to_f16(x0[i]) | ((uint32_t)f32_to_f16(x1[i]) << 16);
     return;
   }
-  rms_apply<kHcPer>(x, D, norm_eps, norm_w, out + p * D, red);
+  rms_pairs(x0, x1, D, norm_eps, norm_w, out + p * D, red);
 }
 
 __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t *__restrict__ xin, int D, const uint16_t *__restrict__ w,
                                                   float eps, uint16_t *__restrict__ y) {
   __shared__ float red[4];
   const int64_t p = blockIdx.x;
-  float x[kHcPer];
+  float x0[kHcPairs], x1[kHcPairs];
 #pragma unroll
-  for (int i = 0; i < kHcPer; ++i) {
-    const int d = threadIdx.x + 256 * i;
-    x[i] = d < D ? h2f(xin[p * D + d]) : 0.0f;
+  for (int i = 0; i < kHcPairs; ++i) {
+    const uint32_t v = pair_d(i) < D ? *reinterpret_cast<const uint32_t *>(xin + p * D + pair_d(i)) : 0u;
+    x0[i] = h2f(v & 0xffff);
+    x1[i] = h2f(v >> 16);
   }
-  rms_apply<kHcPer>(x, D, eps, w, y + p * D, red);
+  rms_pairs(x0, x1, D, eps, w, y + p * D, red);
 }
 
 // post[n] * out + comb^T @ residual, f16 as the reference (its g5_hc_mix runs in
@@ -249,7 +308,7 @@ exl3_status check_hc(const exl3_hc_site *hc, int D) {
     return fail(EXL3_ERR_UNSUPPORTED, "hc_mult must be 1..4 (the fused path's range)");
   if (hc->sinkhorn_iters < 1) return fail(EXL3_ERR_INVALID, "hc_sinkhorn_iters must be >= 1");
   if (D <= 0 || D > kHcMaxD || D % 2 || ((int64_t)hc->mult * D) % kHcChunk)
-    return fail(EXL3_ERR_UNSUPPORTED, "hidden size must be even, at most 8192, and N*hidden a multiple of 256");
+    return fail(EXL3_ERR_UNSUPPORTED, "hidden size must be even, at most 8192, and N*hidden a multiple of 64");
   return EXL3_OK;
 }
 
@@ -296,18 +355,21 @@ exl3_status exl3_hc_prepare(const exl3_hc_site *hc, const uint16_t *streams, int
     return fail(EXL3_ERR_WORKSPACE, "exl3_hc_prepare: workspace too small: need " + std::to_string(need) + " bytes");
   if (reinterpret_cast<uintptr_t>(workspace) % 256)
     return fail(EXL3_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  if (reinterpret_cast<uintptr_t>(streams) % 8 || reinterpret_cast<uintptr_t>(hc->fn) % 16)
-    return fail(EXL3_ERR_INVALID, "streams must be 8-byte and fn 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(streams) % 8 || reinterpret_cast<uintptr_t>(hc->fn) % 16 ||
+      (reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(norm_w)) % 4)
+    return fail(EXL3_ERR_INVALID, "streams must be 8-byte, fn 16-byte, out and norm_w 4-byte aligned");
   return launch_hc_prepare(hc, streams, P, hidden, norm_w, norm_eps, out, post, comb, (float *)workspace,
                            stream_of(stream));
 }
 
 exl3_status exl3_rms_norm(const uint16_t *x, int64_t P, int32_t hidden, const uint16_t *w, float eps, uint16_t *y,
                           exl3_stream_t stream) {
-  if (P < 0 || P > ((int64_t)1 << 31) || hidden <= 0 || hidden > kHcMaxD)
-    return fail(EXL3_ERR_INVALID, "exl3_rms_norm: bad shape (hidden at most 8192)");
+  if (P < 0 || P > ((int64_t)1 << 31) || hidden <= 0 || hidden > kHcMaxD || hidden % 2)
+    return fail(EXL3_ERR_INVALID, "exl3_rms_norm: bad shape (hidden even, at most 8192)");
   if (P == 0) return EXL3_OK;
   if (!x || !w || !y) return fail(EXL3_ERR_INVALID, "exl3_rms_norm: null argument");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(y)) % 4)
+    return fail(EXL3_ERR_INVALID, "exl3_rms_norm: x, w and y must be 4-byte aligned");
   k_rms_norm<<<(unsigned)P, 256, 0, stream_of(stream)>>>(x, hidden, w, eps, y);
   EXL3_LAUNCHED("k_rms_norm");
   return EXL3_OK;

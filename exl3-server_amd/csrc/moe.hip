@@ -870,9 +870,12 @@ int gu_items_default() {
   static const int v = env_items("EXL3_MOE_ITEMS_GU", 2);
   return v;
 }
-int dn_items_default() {
-  static const int v = env_items("EXL3_MOE_ITEMS_DN", 2);
-  return v;
+// Down: one 128-column block per workgroup for single-row calls (256 workgroups of two
+// blocks leave most SIMDs with one wave: 43.7 -> 41.9 us per GLM-5 layer call at B=1),
+// two from 2 rows on. EXL3_MOE_ITEMS_DN (read once) overrides both.
+int dn_items_default(int64_t N) {
+  static const int v = env_items("EXL3_MOE_ITEMS_DN", 0);
+  return v > 0 ? v : (N <= 1 ? 1 : 2);
 }
 
 MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
@@ -942,7 +945,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.pass_rows = (int)std::min<int64_t>(N, 16);
   a.xrot_rows = !a.fold && N >= xrot_min_rows();
   a.gu_items = gu_items_default();
-  a.dn_items = dn_items_default();
+  a.dn_items = dn_items_default(N);
   a.h = h;
   a.router_w = L->router_w;
   a.router_bias = L->router_bias;
@@ -1482,8 +1485,8 @@ exl3_status exl3_moe_block(exl3_moe_layer_t layer, const exl3_hc_site *hc, const
   if (!norm_w || !streams || !streams_out) return fail(EXL3_ERR_INVALID, "null block argument");
   if (P > (1 << 24) / layer->topk) return fail(EXL3_ERR_UNSUPPORTED, "too many rows in one call");
   if (reinterpret_cast<uintptr_t>(streams) % 8 || reinterpret_cast<uintptr_t>(streams_out) % 4 ||
-      reinterpret_cast<uintptr_t>(hc->fn) % 16)
-    return fail(EXL3_ERR_INVALID, "streams must be 8-byte, streams_out 4-byte and fn 16-byte aligned");
+      reinterpret_cast<uintptr_t>(norm_w) % 4 || reinterpret_cast<uintptr_t>(hc->fn) % 16)
+    return fail(EXL3_ERR_INVALID, "streams must be 8-byte, streams_out and norm_w 4-byte, fn 16-byte aligned");
   if (overlaps(streams, streams_out, (size_t)P * hc->mult * layer->H * 2))
     return fail(EXL3_ERR_INVALID, "streams_out must not overlap streams");
   const MoeLayout m = moe_layout(layer, P);

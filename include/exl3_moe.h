@@ -316,13 +316,14 @@ typedef struct {
  * streams (P, mult, hidden) f16 (8-byte aligned) -> out (P, hidden) f16: the collapsed
  * stream sum_n pre[n] * streams[n], or rms_norm(collapsed) * norm_w; post (P, mult) and
  * comb (P, mult, mult) f32 as the reference returns them. The workspace holds k-split
- * partials (exl3_hc_workspace_size). Requires mult * hidden % 256 == 0, hidden <= 8192. */
+ * partials (exl3_hc_workspace_size). Requires mult * hidden % 64 == 0, hidden even and <= 8192. */
 size_t exl3_hc_workspace_size(int32_t mult, int32_t hidden, int64_t P);
 exl3_status exl3_hc_prepare(const exl3_hc_site *hc, const uint16_t *streams, int64_t P, int32_t hidden,
                             const uint16_t *norm_w, float norm_eps, uint16_t *out, float *post, float *comb,
                             void *workspace, size_t workspace_bytes, exl3_stream_t stream);
 /* Replaces rms_norm (glm5_attn.cpp:12-22): y = f16(f16(x * rsqrt(mean(x^2) + eps)) * w),
- * f32 statistics; x, y (P, hidden) f16, w (hidden) f16; hidden <= 8192. */
+ * f32 statistics; x, y (P, hidden) f16, w (hidden) f16, 4-byte aligned; hidden even,
+ * <= 8192. */
 exl3_status exl3_rms_norm(const uint16_t *x, int64_t P, int32_t hidden, const uint16_t *w, float eps,
                           uint16_t *y, exl3_stream_t stream);
 /* Replaces g5_hc_mix (glm5_hc.cpp:342-355): out[p][n] = post[p][n] * block_out[p] +

@@ -244,7 +244,7 @@ def test_block_argument_errors(dev):
     with pytest.raises(_lib.Exl3Error, match="hc_mult"):
         hc_prepare(torch.zeros(1, 5, D, dtype=torch.float16, device=dev), bad)
     odd = DeviceHcSite(3, 20, EPS, site.fn, site.base, site.scale)
-    with pytest.raises(_lib.Exl3Error, match="multiple of 256"):
+    with pytest.raises(_lib.Exl3Error, match="multiple of 64"):
         hc_prepare(torch.zeros(1, 3, 200, dtype=torch.float16, device=dev), odd)
     # zero positions: nothing to do
     assert moe_block(d, site, nw, NORM_EPS, st[:0]).numel() == 0
