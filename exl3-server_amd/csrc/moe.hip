@@ -651,6 +651,15 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   const int c = cb * 128 + 2 * lane;
   const int n_sl = a.fold ? 1 : n_slices(a.I / 16);  // down partials per output
   const int64_t plane = a.H;  // floats between slice planes of one slot
+  // the f16 shared expert's down partials (addresses known at entry): in flight with the
+  // first round of the ranks' loads
+  static_assert(kDenseSlots == 8, "two outputs' partials are four float4");
+  float4 dsh[4];
+  if (a.shared_kind == exl3m::kSharedDense) {
+    const float4 *pd = reinterpret_cast<const float4 *>(a.dsh_dn + ((int64_t)row * a.H + c) * kDenseSlots);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dsh[q] = pd[q];
+  }
   float r0 = 0.0f, r1 = 0.0f;
   for (int k0 = 0; k0 < a.topk; k0 += kCombineBatch) {
     const int nk = min(kCombineBatch, a.topk - k0);
@@ -727,10 +736,19 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     r0 += y0;
     r1 += y1;
   } else if (a.shared_kind == exl3m::kSharedDense) {
-    const float *pd = a.dsh_dn + ((int64_t)row * a.H + c) * kDenseSlots;
+    // dense_slots_sum's order over the two outputs' kDenseSlots partials
     const int S = dense_mfma_splits(a.SI);
-    r0 += rf16(dense_slots_sum(pd, S));
-    r1 += rf16(dense_slots_sum(pd + kDenseSlots, S));
+    const float v0[8] = {dsh[0].x, dsh[0].y, dsh[0].z, dsh[0].w, dsh[1].x, dsh[1].y, dsh[1].z, dsh[1].w};
+    const float v1[8] = {dsh[2].x, dsh[2].y, dsh[2].z, dsh[2].w, dsh[3].x, dsh[3].y, dsh[3].z, dsh[3].w};
+    float d0 = v0[0], d1 = v1[0];
+#pragma unroll
+    for (int q = 1; q < 8; ++q)
+      if (q < S) {
+        d0 += v0[q];
+        d1 += v1[q];
+      }
+    r0 += rf16(d0);
+    r1 += rf16(d1);
   }
   const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(r0)) |
                      ((uint32_t)bitcast<uint16_t>(to_f16(r1)) << 16);
