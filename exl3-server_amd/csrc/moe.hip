@@ -888,12 +888,14 @@ int gu_items_default() {
   static const int v = env_items("EXL3_MOE_ITEMS_GU", 2);
   return v;
 }
-// Down: one 128-column block per workgroup for single-row calls (256 workgroups of two
-// blocks leave most SIMDs with one wave: 43.7 -> 41.9 us per GLM-5 layer call at B=1),
-// two from 2 rows on. EXL3_MOE_ITEMS_DN (read once) overrides both.
+// Down: one 128-column block per workgroup (GLM-5 layer: at B=1, 43.7 -> 41.9 us per
+// call, where 256 workgroups of two blocks leave most SIMDs one wave; at B=8 the down
+// launch 1.0-1.6 us shorter than with two blocks in three A/B runs, three blocks slower).
+// EXL3_MOE_ITEMS_DN (read once) overrides it.
 int dn_items_default(int64_t N) {
-  static const int v = env_items("EXL3_MOE_ITEMS_DN", 0);
-  return v > 0 ? v : (N <= 1 ? 1 : 2);
+  (void)N;
+  static const int v = env_items("EXL3_MOE_ITEMS_DN", 1);
+  return v;
 }
 
 MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
