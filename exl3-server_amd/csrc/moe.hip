@@ -876,6 +876,17 @@ int64_t xrot_min_rows() {
   return v;
 }
 
+// Token rows staged per pass of the short-run expert kernels (at most 16, one MFMA row
+// block): EXL3_MOE_PASS_ROWS, read once. Runs longer than a pass take several passes.
+int pass_rows_cap() {
+  static const int v = [] {
+    const char *e = std::getenv("EXL3_MOE_PASS_ROWS");
+    const int x = e ? std::atoi(e) : 0;
+    return x >= 1 && x <= 16 ? x : 16;
+  }();
+  return v;
+}
+
 // 128-column blocks per short-run expert workgroup (one ring-word stream per wave over
 // the group): EXL3_MOE_ITEMS_GU / EXL3_MOE_ITEMS_DN, read once. No output bit depends on
 // them.
@@ -962,7 +973,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.logit_splits = dense_mfma_splits(a.H);
   a.n_logit_blocks = (int)dense_mfma_tasks(N, a.H, a.E);  // one task per workgroup
   a.fold = N >= long_min_rows();  // long runs: kLongRows-row passes, slices folded
-  a.pass_rows = (int)std::min<int64_t>(N, 16);
+  a.pass_rows = (int)std::min<int64_t>(N, pass_rows_cap());
   a.xrot_rows = !a.fold && N >= xrot_min_rows();
   a.gu_items = gu_items_default();
   a.dn_items = dn_items_default(N);
