@@ -190,6 +190,7 @@ __global__ __launch_bounds__(256) void k_moe_pre_tiled(MoeArgs a) {
 // Routing + dispatch, one workgroup of 16 waves (glm5_moe.cpp:16-60, 158-255).
 // ---------------------------------------------------------------------------------
 constexpr int kMaxE = 1024;
+constexpr int kIdBatch = 16;  // pair experts per lane loaded at once by the counting sort
 // Route kernels are instantiated for E <= 64 * JN experts (JN 64-expert chunks per lane).
 template <typename F>
 static void with_route_chunks(int E, F &&f) {
@@ -512,13 +513,26 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
   const int P = a.P;
   const int seg = ((P + 15) / 16 + 63) / 64 * 64;
   const int pbeg = wave * seg, pend = min(P, pbeg + seg);
-  for (int c = pbeg; c < pend; c += 64) {
-    const int p = c + lane;
-    const bool valid = p < pend;
-    const int e = valid ? id_out[p] : 0;
-    const uint64_t m = match_mask(e, valid);
-    if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
-    __builtin_amdgcn_wave_barrier();
+  // A wave's pairs go 64 at a time; their experts are loaded kIdBatch rounds at once (the
+  // addresses clamped, so that no branch separates the loads): one memory round trip
+  // per batch instead of one per round.
+  auto load_ids = [&](int c0, int (&ev)[kIdBatch]) {
+#pragma unroll
+    for (int q = 0; q < kIdBatch; ++q) ev[q] = id_out[min(c0 + 64 * q + lane, P - 1)];
+  };
+  for (int c0 = pbeg; c0 < pend; c0 += 64 * kIdBatch) {
+    int ev[kIdBatch];
+    load_ids(c0, ev);
+#pragma unroll
+    for (int q = 0; q < kIdBatch; ++q) {
+      if (c0 + 64 * q >= pend) break;
+      const int p = c0 + 64 * q + lane;
+      const bool valid = p < pend;
+      const int e = valid ? ev[q] : 0;
+      const uint64_t m = match_mask(e, valid);
+      if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
+      __builtin_amdgcn_wave_barrier();
+    }
   }
   __syncthreads();
   // Per expert: total, base offset (exclusive scan over experts), per-wave offsets.
@@ -598,22 +612,28 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
     *a.n_passes = npas;
   }
   __syncthreads();
-  for (int c = pbeg; c < pend; c += 64) {
-    const int p = c + lane;
-    const bool valid = p < pend;
-    const int e = valid ? id_out[p] : 0;
-    const uint64_t m = match_mask(e, valid);
-    if (valid) {
-      const int pos = cnt[wave * kMaxE + e] + __builtin_popcountll(m & lanes_below());
-      a.sorted_row[pos] = p / K;
-      a.sorted_rank[pos] = p % K;
-      a.slot_e[pos] = e;
-      a.slot[p] = pos;
-      if (pos == s_base[e]) a.run_rec[s_run_of[e]].row0 = p / K;
+  for (int c0 = pbeg; c0 < pend; c0 += 64 * kIdBatch) {
+    int ev[kIdBatch];
+    load_ids(c0, ev);
+#pragma unroll
+    for (int q = 0; q < kIdBatch; ++q) {
+      if (c0 + 64 * q >= pend) break;
+      const int p = c0 + 64 * q + lane;
+      const bool valid = p < pend;
+      const int e = valid ? ev[q] : 0;
+      const uint64_t m = match_mask(e, valid);
+      if (valid) {
+        const int pos = cnt[wave * kMaxE + e] + __builtin_popcountll(m & lanes_below());
+        a.sorted_row[pos] = p / K;
+        a.sorted_rank[pos] = p % K;
+        a.slot_e[pos] = e;
+        a.slot[p] = pos;
+        if (pos == s_base[e]) a.run_rec[s_run_of[e]].row0 = p / K;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
-    if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
-    __builtin_amdgcn_wave_barrier();
   }
   for (int i = threadIdx.x; i < a.N; i += 1024) {
     a.sorted_row[P + i] = i;
