@@ -359,37 +359,45 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
   const int jn = (E + 63) / 64;
   const int S = a.logit_splits;  // 0: plain logits (N, E); else S partials in (N, E, 8)
   for (int b = (mode & 1) ? blockIdx.x * 16 + wave : a.N; b < a.N; b += 16 * gridDim.x) {
-    // all logit partial and bias loads first (clamped addresses, so no branches split
-    // them), then the split sums in split order, the sigmoid and the biased score
+    // the logit partial and bias loads of kLoadJ chunks at once (clamped addresses, so
+    // no branches split them; every chunk at once up to 320 experts, 4 at a time above,
+    // which keeps the partials in registers), then the split sums in split order, the
+    // sigmoid and the biased score
+    constexpr int kLoadJ = kJ <= 5 ? kJ : 4;
+    static_assert(kJ % kLoadJ == 0, "route chunks");
     float sc[kJ], sfc[kJ];
-    float4 lp[kJ][2];
-    float bias[kJ];
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const int e = min(lane + 64 * j, E - 1);
-      if (S == 0) {
-        lp[j][0].x = a.logits[(int64_t)b * E + e];
-      } else {
-        const float4 *q = reinterpret_cast<const float4 *>(a.logits + ((int64_t)b * E + e) * kDenseSlots);
-        lp[j][0] = q[0];
-        lp[j][1] = q[1];
+    for (int j0 = 0; j0 < kJ; j0 += kLoadJ) {
+      float4 lp[kLoadJ][2];
+      float bias[kLoadJ];
+#pragma unroll
+      for (int jj = 0; jj < kLoadJ; ++jj) {
+        const int e = min(lane + 64 * (j0 + jj), E - 1);
+        if (S == 0) {
+          lp[jj][0].x = a.logits[(int64_t)b * E + e];
+        } else {
+          const float4 *q = reinterpret_cast<const float4 *>(a.logits + ((int64_t)b * E + e) * kDenseSlots);
+          lp[jj][0] = q[0];
+          lp[jj][1] = q[1];
+        }
+        bias[jj] = a.router_bias[e];
       }
-      bias[j] = a.router_bias[e];
-    }
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const float v[8] = {lp[j][0].x, lp[j][0].y, lp[j][0].z, lp[j][0].w,
-                          lp[j][1].x, lp[j][1].y, lp[j][1].z, lp[j][1].w};
-      float lg = v[0];
+      for (int jj = 0; jj < kLoadJ; ++jj) {
+        const int j = j0 + jj;
+        const float v[8] = {lp[jj][0].x, lp[jj][0].y, lp[jj][0].z, lp[jj][0].w,
+                            lp[jj][1].x, lp[jj][1].y, lp[jj][1].z, lp[jj][1].w};
+        float lg = v[0];
 #pragma unroll
-      for (int s = 1; s < 8; ++s)
-        if (s < S) lg += v[s];
-      const int e = lane + 64 * j;
-      sc[j] = 0.0f;
-      sfc[j] = -INFINITY;
-      if (e < E) {
-        sc[j] = 1.0f / (1.0f + expf(-lg));
-        sfc[j] = sc[j] + bias[j];
+        for (int s = 1; s < 8; ++s)
+          if (s < S) lg += v[s];
+        const int e = lane + 64 * j;
+        sc[j] = 0.0f;
+        sfc[j] = -INFINITY;
+        if (e < E) {
+          sc[j] = 1.0f / (1.0f + expf(-lg));
+          sfc[j] = sc[j] + bias[jj];
+        }
       }
     }
     if (ng > 1) {
