@@ -462,6 +462,42 @@ def test_prefill_2048_config5(oracle, dev):
     d.close()
 
 
+def test_dispatch_many_pairs(oracle, dev):
+    # 2600 rows x top-8 = 20800 pairs: past 16384, so that each of the counting sort's
+    # waves takes its pairs' experts in two batches (16 rounds of 64, then 5), with hot
+    # experts whose runs need several 48-row passes; small tensors keep it quick
+    cfg = synth.MoeConfig(hidden=256, inter=128, n_experts=64, top_k=8, routed_scaling_factor=2.0,
+                          shared_inter=128, gate_up_K=3, gate_up_cb=1, down_K=2, down_cb=2, shared_K=0)
+    hot = [3, 17, 40]
+    layer, words = glm5_layer_on_device(dev, 61, "many", cfg, hot, 0.3)
+    N, H = 2600, cfg.hidden
+    h = synth.activations(61, "many.x", N, H)
+    x = to_dev(h, dev, N, 1, H)
+    d = DeviceMoeLayer(layer, dev, words=words)
+    d.diag_enable()
+    y = d(x).view(N, H)
+    _, ids = d.route(x)
+    oc = ocfg_of(oracle, cfg, True)
+    logits = oracle.router_logits(h, layer.router_w)
+    idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+    runs = oracle.moe_runs(idx)
+    assert max(runs["run_len"]) > 2 * 48
+    hist = {}
+    for r in runs["run_len"].tolist():
+        hist[min(r, 64)] = hist.get(min(r, 64), 0) + 1
+    assert d.diag()["run_hist"] == hist
+    check_diag_bytes(d.diag(), runs["run_len"], cfg, 48)
+    rows = sorted(set(list(range(0, N, 157)) + [N - 1]))
+    yc = y.cpu()
+    for r in rows:
+        assert torch.equal(d(x[r:r + 1].contiguous()).view(-1).cpu(), yc[r]), r
+    used = set(idx[rows].reshape(-1).tolist())
+    want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used), oracle_shared(layer, words),
+                                   h[rows], idx[rows], w[rows])
+    check_out(yc[rows], want)
+    d.close()
+
+
 @pytest.mark.parametrize("gu_K,gu_cb,dn_K,dn_cb", [(1, 0, 2, 1), (2, 2, 3, 0), (3, 1, 6, 2), (5, 0, 7, 1),
                                                    (6, 2, 8, 0), (7, 1, 1, 2), (8, 0, 4, 1)])
 def test_layer_k_codebook_sweep(oracle, dev, gu_K, gu_cb, dn_K, dn_cb):
