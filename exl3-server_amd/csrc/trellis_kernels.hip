@@ -148,9 +148,12 @@ __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_
                                              int pass_rows, float *__restrict__ part,
                                              exl3h::PtrTable suh, int rotate) {
   constexpr bool kDup = dup_cb(CB);
-  // the largest slice's staged rows, then one ring-word slot per wave
-  __shared__ uint32_t xs[kPassRows * (kMaxSliceSteps * kStepTiles * tile_words(kDup) + 4)];
-  __shared__ u32x4 slots[4 * slot_chunks(K)];
+  // one ring-word slot per wave, then the slice's staged rows (pass_rows of them: the
+  // launch sizes the LDS to the pass, so a one-row call is not held to the occupancy of
+  // a 16-row one)
+  extern __shared__ u32x4 qmv_smem[];
+  u32x4 *slots = qmv_smem;
+  uint32_t *xs = reinterpret_cast<uint32_t *>(qmv_smem + 4 * slot_chunks(K));
   const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
   const int slice_k = kStepTiles * ss * 16, xs_stride = staged_row_words(k_tiles, kDup);
   // grid: x = 128-column block, y = row block * n_sl + k-slice, z = member (one row
@@ -318,8 +321,12 @@ template <int K, int CB, int PD>
 static void qmv_go(dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, int in, int out,
                    const uint16_t *xhat, int64_t xs, int64_t rows, int pass_rows, float *part,
                    const PtrTable *suh) {
-  k_qmv<K, CB, PD><<<grid, 256, 0, st>>>(tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part,
-                                         suh ? *suh : PtrTable{}, suh ? 1 : 0);
+  // the wave slots and pass_rows staged rows (at most 16 x 2 KB + 8 KB: under the 64 KB
+  // that a launch gets without an attribute)
+  const size_t lds = (size_t)4 * slot_chunks(K) * 16 +
+                     (size_t)pass_rows * staged_row_words(in / 16, dup_cb(CB)) * 4;
+  k_qmv<K, CB, PD><<<grid, 256, lds, st>>>(tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part,
+                                           suh ? *suh : PtrTable{}, suh ? 1 : 0);
 }
 
 template <int K, int CB>
