@@ -323,6 +323,10 @@ static void qmv_go(dim3 grid, hipStream_t st, const PtrTable &tr, int tiles_n, i
                    const PtrTable *suh) {
   // the wave slots and pass_rows staged rows (at most 16 x 2 KB + 8 KB: under the 64 KB
   // that a launch gets without an attribute)
+  static_assert((size_t)4 * slot_chunks(8) * 16 +
+                    (size_t)kPassRows * (kMaxSliceSteps * kStepTiles * tile_words(true) + 4) * 4 <=
+                64 * 1024,
+                "k_qmv LDS");
   const size_t lds = (size_t)4 * slot_chunks(K) * 16 +
                      (size_t)pass_rows * staged_row_words(in / 16, dup_cb(CB)) * 4;
   k_qmv<K, CB, PD><<<grid, 256, lds, st>>>(tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part,
