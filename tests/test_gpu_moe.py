@@ -215,19 +215,20 @@ def test_repeat_calls_are_deterministic(dev):
     d.close()
 
 
-@pytest.mark.parametrize("H,E", [(384, 72), (512, 64), (1280, 130), (4096, 96), (8192, 40)])
+@pytest.mark.parametrize("H,E", [(384, 72), (512, 64), (1280, 130), (4096, 96), (8192, 40), (4096, 288)])
 def test_tiled_router_logits_equal_single_row(dev, H, E):
     # calls of 256 rows or more compute the router logits in 64 x 64 tiles (k splits of
-    # 1, 4, 2, 8 and 8 here; 1280 ends a quarter on a partial staging round, 8192 takes
-    # two rounds per quarter); the routing weights, f32 functions of the logits, equal
-    # the single-row (untiled) calls' bit for bit, and the rows past the last full
-    # 64-row tile are routed like the rest
+    # 1, 4, 2, 8, 8 and 8 here; 1280 ends a quarter on a partial staging round, 8192
+    # takes two rounds per quarter; 130 and 288 experts end on partial expert tiles);
+    # the routing weights, f32 functions of the logits, equal the single-row (untiled)
+    # calls' bit for bit, and the rows past the last full 64-row tile are routed like
+    # the rest
     cfg = synth.MoeConfig(hidden=H, inter=128, n_experts=E, top_k=4, routed_scaling_factor=2.5)
     d = DeviceMoeLayer(synth.make_layer(cfg, 61, tag=f"tile{H}"), dev)
     N = 300
     x = to_dev(synth.activations(61, f"tile.x.{H}", N, H), dev, N, 1, H)
     w, ids = d.route(x)
-    for r in (0, 1, 63, 64, 130, 255, 256, 299):
+    for r in (0, 1, 63, 64, 127, 128, 130, 255, 256, 299):
         w1, i1 = d.route(x[r:r + 1].contiguous())
         assert torch.equal(i1.view(-1), ids[r].view(-1)), r
         assert torch.equal(w1.view(-1), w[r].view(-1)), r
