@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """bench.py -- EXL3 MoE decode layer on one MI355X.
 
-Metric (BASELINE.json): MoE-layer decode tokens/s + achieved HBM GB/s on trellis bytes,
+Metric: MoE-layer decode tokens/s + achieved HBM GB/s on trellis bytes,
 B=8, 1 MI355X. Workload: GLM-5-shaped layer -- hidden 4096, expert
 intermediate 1024, 288 experts, top-8 sigmoid routing with a selection-only correction
 bias, routed_scaling_factor 2.5, swiglu_limit 10, gate/up K4 mcg, down K5 mcg, fp16
