@@ -21,6 +21,7 @@
 
 #include <cmath>
 #include <string>
+#include <type_traits>
 
 #include "exl3_device.hpp"
 #include "exl3_internal.hpp"
@@ -172,12 +173,12 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
     float acc = 0.0f;
     if (j < W || j == kHcMaxW) {
       const float *pp = part + p * n_chunks * kHcVals + j;
-      for (int c0 = g; c0 < n_chunks; c0 += 8 * 16) {
-        float v[16];
+      for (int c0 = g; c0 < n_chunks; c0 += 8 * 32) {
+        float v[32];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) v[q] = pp[(int64_t)min(c0 + 8 * q, n_chunks - 1) * kHcVals];
+        for (int q = 0; q < 32; ++q) v[q] = pp[(int64_t)min(c0 + 8 * q, n_chunks - 1) * kHcVals];
 #pragma unroll
-        for (int q = 0; q < 16; ++q)
+        for (int q = 0; q < 32; ++q)
           if (c0 + 8 * q < n_chunks) acc += v[q];
       }
     }
@@ -192,8 +193,10 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
   }
   __syncthreads();
   if (t < 64) {
-    // wave 0, one lane per value: lane l < N*N holds comb entry (l / N, l % N); row and
-    // column reductions gather the N entries by shuffles, in index order
+    // wave 0: lane l < 16 holds comb entry (l / 4, l % 4) of a 4 x 4 layout (entries
+    // outside N x N stay 0), so a row is a quad and a column the lanes j, j + 4, j + 8,
+    // j + 12 of the first 16: row sums by quad-permute DPP, column sums by row-rotate DPP,
+    // no LDS round trip per reduction
     const float rms = 1.0f / sqrtf(vals[kHcMaxW] / (float)ND + eps);
     const int lane = t;
     if (lane < N) {
@@ -201,47 +204,39 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
       pre[lane] = 1.0f / (1.0f + expf(-(wp * scale[0] + base[lane]))) + eps;
       post_out[p * N + lane] = 2.0f * (1.0f / (1.0f + expf(-(wq * scale[1] + base[N + lane]))));
     }
-    const int NN = N * N;
-    const bool live = lane < NN;
-    const int ci = live ? lane / N : 0, cj = live ? lane % N : 0;
-    const float z = live ? vals[2 * N + lane] * rms * scale[2] + base[2 * N + lane] : 0.0f;
+    const int ci = (lane >> 2) & 3, cj = lane & 3;
+    const bool live = lane < 16 && ci < N && cj < N;
+    auto dpp = [](float v, auto ctrl) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), decltype(ctrl)::value,
+                                                                 0xF, 0xF, false));
+    };
+    using X1 = std::integral_constant<int, 0xB1>;   // lane ^ 1
+    using X2 = std::integral_constant<int, 0x4E>;   // lane ^ 2
+    using R4 = std::integral_constant<int, 0x124>;  // rotate right by 4 within 16 lanes
+    using R8 = std::integral_constant<int, 0x128>;  // rotate right by 8 within 16 lanes
     auto row_sum = [&](float v) {
-      float o[kHcMaxN];
-#pragma unroll
-      for (int k = 0; k < kHcMaxN; ++k) o[k] = __shfl(v, ci * N + min(k, N - 1), 64);
-      float s = o[0];
-#pragma unroll
-      for (int k = 1; k < kHcMaxN; ++k)
-        if (k < N) s += o[k];
-      return s;
+      const float s = v + dpp(v, X1{});
+      return s + dpp(s, X2{});
     };
     auto col_sum = [&](float v) {
-      float o[kHcMaxN];
-#pragma unroll
-      for (int k = 0; k < kHcMaxN; ++k) o[k] = __shfl(v, min(k, N - 1) * N + cj, 64);
-      float s = o[0];
-#pragma unroll
-      for (int k = 1; k < kHcMaxN; ++k)
-        if (k < N) s += o[k];
-      return s;
+      const float s = v + dpp(v, R4{});
+      return s + dpp(s, R8{});
     };
     // softmax over the last axis (j), then + eps
-    float o[kHcMaxN];
-#pragma unroll
-    for (int k = 0; k < kHcMaxN; ++k) o[k] = __shfl(z, ci * N + min(k, N - 1), 64);
-    float m = o[0];
-#pragma unroll
-    for (int k = 1; k < kHcMaxN; ++k)
-      if (k < N) m = fmaxf(m, o[k]);
-    float c = expf(z - m);
-    c = c / row_sum(c) + eps;
-    // Sinkhorn: columns, then (iters - 1) x (rows, columns)
+    const float z = live ? vals[2 * N + ci * N + cj] * rms * scale[2] + base[2 * N + ci * N + cj] : -INFINITY;
+    float m = fmaxf(z, dpp(z, X1{}));
+    m = fmaxf(m, dpp(m, X2{}));
+    float c = live ? expf(z - m) : 0.0f;
+    const float rs = row_sum(c);
+    c = live ? c / rs + eps : 0.0f;
+    // Sinkhorn: columns, then (iters - 1) x (rows, columns); the entries outside N x N
+    // are 0 and stay 0
     c = c / (col_sum(c) + eps);
     for (int it = 0; it < iters - 1; ++it) {
       c = c / (row_sum(c) + eps);
       c = c / (col_sum(c) + eps);
     }
-    if (live) comb_out[p * NN + lane] = c;
+    if (live) comb_out[p * N * N + ci * N + cj] = c;
   }
   __syncthreads();
   // collapsed = sum_n pre[n] * streams[n], in f16
