@@ -116,15 +116,18 @@ constexpr int kHcPairs = kHcMaxD / 512;  // element pairs per thread at the larg
 // This thread's pairs of a row: d = 2 * (threadIdx.x + 256 * i).
 __device__ __forceinline__ int pair_d(int i) { return 2 * ((int)threadIdx.x + 256 * i); }
 
-// y = f16(f16(x * r) * w) on this thread's pairs (x0/x1: the pairs' f16 values in f32),
-// r = rsqrt(mean(x^2) + eps) of the row: the thread's squares summed in pair order, then
-// the workgroup's sum. The norm weights' loads are issued first.
-__device__ __forceinline__ void rms_pairs(const float (&x0)[kHcPairs], const float (&x1)[kHcPairs], int D,
-                                          float eps, const uint16_t *w, uint16_t *y, float *red) {
-  uint32_t wv[kHcPairs];
+// This thread's pairs of the norm weights (w: at least D values; callers issue these
+// loads early, so that they are not a round trip of their own at the end).
+__device__ __forceinline__ void load_pairs(const uint16_t *w, int D, uint32_t (&wv)[kHcPairs]) {
 #pragma unroll
-  for (int i = 0; i < kHcPairs; ++i)
-    wv[i] = pair_d(i) < D ? *reinterpret_cast<const uint32_t *>(w + pair_d(i)) : 0u;
+  for (int i = 0; i < kHcPairs; ++i) wv[i] = *reinterpret_cast<const uint32_t *>(w + min(pair_d(i), D - 2));
+}
+
+// y = f16(f16(x * r) * w) on this thread's pairs (x0/x1: the pairs' f16 values in f32;
+// wv: the norm weights' pairs, from load_pairs), r = rsqrt(mean(x^2) + eps) of the row:
+// the thread's squares summed in pair order, then the workgroup's sum.
+__device__ __forceinline__ void rms_pairs(const float (&x0)[kHcPairs], const float (&x1)[kHcPairs], int D,
+                                          float eps, const uint32_t (&wv)[kHcPairs], uint16_t *y, float *red) {
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < kHcPairs; ++i)
@@ -165,6 +168,10 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
     for (int i = 0; i < kHcPairs; ++i)
       sp[n][i] = n < N && pair_d(i) < D ? *reinterpret_cast<const uint32_t *>(srow + (int64_t)n * D + pair_d(i))
                                         : 0u;
+  // the norm weights too (the row's own streams stand in when there is no norm: same
+  // length, never used)
+  uint32_t wv[kHcPairs];
+  load_pairs(norm_w ? norm_w : srow, D, wv);
   // the chunk partials: thread (g, j) sums value j over chunks g, g + 8, ... in order
   // (their loads in flight together), then value j is the sum of the 8 group sums in
   // group order
@@ -261,7 +268,7 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
             (uint32_t)f32_to_f16(x0[i]) | ((uint32_t)f32_to_f16(x1[i]) << 16);
     return;
   }
-  rms_pairs(x0, x1, D, norm_eps, norm_w, out + p * D, red);
+  rms_pairs(x0, x1, D, norm_eps, wv, out + p * D, red);
 }
 
 __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t *__restrict__ xin, int D, const uint16_t *__restrict__ w,
@@ -269,13 +276,15 @@ __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t *__restrict__ x
   __shared__ float red[4];
   const int64_t p = blockIdx.x;
   float x0[kHcPairs], x1[kHcPairs];
+  uint32_t wv[kHcPairs];
+  load_pairs(w, D, wv);
 #pragma unroll
   for (int i = 0; i < kHcPairs; ++i) {
     const uint32_t v = pair_d(i) < D ? *reinterpret_cast<const uint32_t *>(xin + p * D + pair_d(i)) : 0u;
     x0[i] = h2f(v & 0xffff);
     x1[i] = h2f(v >> 16);
   }
-  rms_pairs(x0, x1, D, eps, w, y + p * D, red);
+  rms_pairs(x0, x1, D, eps, wv, y + p * D, red);
 }
 
 // post[n] * out + comb^T @ residual, f16 as the reference (its g5_hc_mix runs in
