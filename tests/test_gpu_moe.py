@@ -184,6 +184,66 @@ def test_layer_with_shared_experts(oracle, dev):
         d.close()
 
 
+def _moe_test_g_linear(in_f, out_f, byte):
+    # tests/moe_test.cpp:524-545 (mkqg): K3 mul1, every ring word 0x0101 * byte, suh and
+    # svh from the reference's formulas (f32, then f16)
+    K = 3
+    words = np.full(((in_f // 16) * (out_f // 16) * 16 * K,), 0x0101 * (byte & 0xFF), np.uint16)
+    i_in, i_out = np.arange(in_f, dtype=np.uint64), np.arange(out_f, dtype=np.uint64)
+    sc = (np.float32(0.5) + np.float32(0.01) * ((i_in * 13 + byte) % 17).astype(np.float32)).astype(np.float16)
+    sv = (np.float32(0.25) + np.float32(0.01) * ((i_out * 7 + byte) % 13).astype(np.float32)).astype(np.float16)
+    return synth.Linear(in_f, out_f, trellis=words.reshape(in_f // 16, out_f // 16, 16 * K),
+                        suh=sc.view(np.uint16), svh=sv.view(np.uint16), K=K, cb=synth.CB_MUL1)
+
+
+def test_moe_test_g_h_fixture(oracle, dev):
+    # tests/moe_test.cpp:513-653, sections (g) and (h), on their own fixture: hidden and
+    # intermediate 128, 4 experts, top-3, K3 mul1 tensors of byte-uniform ring words
+    # (bytes {9, 31, ..., 199} in turn, the shared expert 9, 31, 49), scaling 1.5, limit
+    # 10, norm_topk_prob; inputs h4[i] = 0.03 ((29 i + 7) mod 31) - 0.4 and
+    # h11[i] = 0.05 ((13 i + 5) mod 37) - 0.7. The router weights follow the test's
+    # formula 0.2 (r mod 100) / 100 - 0.1 on a seeded generator here, not its mt19937
+    # stream. Checks as there: outputs finite and non-zero, the 4- and 11-row calls (33
+    # pairs over 4 experts) equal to single-row calls bit for bit; and, beyond the
+    # reference, the layer against the oracle.
+    GB = (9, 31, 49, 62, 75, 89, 110, 128, 155, 173, 186, 199)
+    H = I = 128
+    E, K = 4, 3
+    cfg = synth.MoeConfig(hidden=H, inter=I, n_experts=E, top_k=K, routed_scaling_factor=1.5,
+                          swiglu_limit=10.0, shared_inter=I, gate_up_K=3, gate_up_cb=synth.CB_MUL1,
+                          down_K=3, down_cb=synth.CB_MUL1, shared_K=3, shared_cb=synth.CB_MUL1)
+    experts = []
+    for e in range(E):
+        for w in range(3):
+            b = GB[(e * 3 + w) % 12]
+            experts.append(_moe_test_g_linear(I, H, b) if w == 2 else _moe_test_g_linear(H, I, b))
+    shared = [_moe_test_g_linear(H, I, 9), _moe_test_g_linear(H, I, 31), _moe_test_g_linear(I, H, 49)]
+    rng = np.random.default_rng(5)
+    gw = (np.float32(0.2) * (rng.integers(0, 1 << 32, E * H) % 100).astype(np.float32) / np.float32(100)
+          - np.float32(0.1)).astype(np.float16).reshape(E, H)
+    gb = (np.float32(0.05) * (rng.integers(0, 1 << 32, E) % 100).astype(np.float32) / np.float32(100))
+    layer = synth.MoeLayer(cfg, experts, shared, gw.view(np.uint16), gb.astype(np.float32))
+    d = DeviceMoeLayer(layer, dev)
+    oc = ocfg_of(oracle, cfg, True)
+    for B, a, m, c, mod in ((4, 0.03, 29, 7, 31), (11, 0.05, 13, 5, 37)):
+        i = np.arange(B * H, dtype=np.int64)
+        hv = (np.float32(a) * ((i * m + c) % mod).astype(np.float32) - np.float32(0.4 if B == 4 else 0.7))
+        h = hv.astype(np.float16).view(np.uint16).reshape(B, H)
+        x = to_dev(h, dev, B, 1, H)
+        yb = d(x)
+        yf = yb.float().cpu()
+        assert torch.isfinite(yf).all() and yf.abs().max() > 1e-3, B
+        for b in range(B):
+            assert torch.equal(d(x[b:b + 1].contiguous()).cpu().view(-1), yb.cpu()[b].view(-1)), (B, b)
+        _, ids = d.route(x)
+        logits = oracle.router_logits(h, layer.router_w)
+        idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+        want = oracle.moe_layer_routed(oc, [l.oracle_dict() for l in experts],
+                                       [l.oracle_dict() for l in shared], h, idx, w)
+        check_out(yb, want)
+    d.close()
+
+
 def test_rows_path_equals_single_rows(dev):
     # moe_test.cpp (g)/(h): 128-wide fixture, 4 experts, top-3, 11 rows (33 pairs,
     # every expert selected several times); the batch equals single-row calls
