@@ -114,6 +114,42 @@ def test_hc_prepare_glm5_scale_streams(oracle, dev):
     check_f16(out, coll, ulps=1, extra=collapse_cond(st))
 
 
+@pytest.mark.parametrize("eps", [1e-3, 0.05])
+@pytest.mark.parametrize("iters", [1, 3, 4, 20])
+def test_hc_prepare_large_eps_and_iteration_count(oracle, dev, eps, iters):
+    # At hc_eps 1e-6 a dropped eps (in the rsqrt, pre, the softmax or any Sinkhorn
+    # denominator) moves post/comb by ~1e-6, inside the 2e-5 bound; at 1e-3 and 0.05 it
+    # moves them by far more. The oracle's iteration count is pinned on the CPU, and 3 and 4
+    # iterations differ by more than the bound for these logits, so matching it at each
+    # count pins the device's count too.
+    P, N, D = 5, 4, 1024
+    fn, base, scale = make_site(90 + iters, N, D)
+    base[2 * N:] = np.random.default_rng(91).uniform(-3, 3, size=N * N).astype(np.float32)
+    st = streams_of(92, P, N, D)
+    site = DeviceHcSite.from_numpy(fn, base, scale, N, iters, eps, dev)
+    out, post, comb = hc_prepare(dev_f16(st, dev), site)
+    coll, opost, ocomb = oracle.hc_prepare(st, N, D, fn, base, scale, iters, eps)
+    assert np.max(np.abs(post.cpu().numpy() - opost)) <= 2e-5
+    assert np.max(np.abs(comb.cpu().numpy() - ocomb)) <= 2e-5
+    check_f16(out, coll, ulps=1, extra=collapse_cond(st))
+
+
+def test_hc_mix_identity_roundtrip(dev):
+    # the reference's expand -> mix identity: streams that are copies of x, post = 1 and
+    # comb = I give out[n] = f16(bo + x) exactly (1 * bo and 1 * x are exact, the sum is
+    # rounded once)
+    P, N, D = 6, 4, 512
+    rng = np.random.default_rng(93)
+    x = rng.normal(size=(P, D)).astype(np.float16)
+    bo = rng.normal(size=(P, D)).astype(np.float16)
+    st = np.ascontiguousarray(np.broadcast_to(x[:, None, :], (P, N, D)))
+    comb = np.broadcast_to(np.eye(N, dtype=np.float32), (P, N, N)).copy()
+    out = hc_mix(torch.from_numpy(bo).to(dev), torch.ones(P, N, device=dev), torch.from_numpy(comb).to(dev),
+                 torch.from_numpy(st).to(dev)).cpu().numpy()
+    want = (bo.astype(np.float32) + x.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(out, np.broadcast_to(want[:, None, :], (P, N, D)))
+
+
 @pytest.mark.parametrize("P,D", [(7, 4096), (3, 1000), (2, 8192), (33, 6144)])
 def test_rms_norm_vs_oracle(oracle, dev, P, D):
     rng = np.random.default_rng(P + D)

@@ -63,8 +63,10 @@ def test_stream_permutation_equivariance(oracle):
         np.abs(c1.view(np.float16).astype(float)).max() * 2 ** -10
 
 
-def test_rms_factor_and_fn_orientation(oracle):
-    # fn one-hot: output j reads element i_j of the flattened (N, D) streams, times the
+@pytest.mark.parametrize("eps", [EPS, 1e-3])
+def test_rms_factor_and_fn_orientation(oracle, eps):
+    # eps 1e-3 makes the eps inside the rsqrt visible (sqrt(ms + eps) vs sqrt(ms) + eps
+    # differ by ~5e-4 at ms ~ 1). fn one-hot: output j reads element i_j of the flattened (N, D) streams, times the
     # RMS factor; with scale 1 and base 0, pre = sigmoid(s[i_j] * rms) + eps
     P, N, D = 2, 2, 40
     streams, fn, base, scale = make(4, P, N, D)
@@ -74,9 +76,9 @@ def test_rms_factor_and_fn_orientation(oracle):
     fn[np.arange(W), idx] = 1
     base[:] = 0
     scale[:] = 1
-    _, post, _ = oracle.hc_prepare(streams, N, D, fn, base, scale, 20, EPS)
+    _, post, _ = oracle.hc_prepare(streams, N, D, fn, base, scale, 20, eps)
     s = streams.reshape(P, N * D).view(np.float16).astype(np.float64)
-    rms = 1 / np.sqrt((s ** 2).mean(1) + EPS)
+    rms = 1 / np.sqrt((s ** 2).mean(1) + eps)
     want_post = 2 / (1 + np.exp(-(s[:, idx[N:2 * N]] * rms[:, None])))
     assert np.allclose(post, want_post, rtol=1e-12)
     # scaling the streams by 2 (exact in f16) leaves post/comb unchanged and doubles the
@@ -90,17 +92,18 @@ def test_rms_factor_and_fn_orientation(oracle):
     assert np.array_equal(c2.view(np.float16), c1.view(np.float16) * np.float16(2))
 
 
-def test_n1_closed_form(oracle):
+@pytest.mark.parametrize("eps", [EPS, 1e-3, 0.05])
+def test_n1_closed_form(oracle, eps):
     P, D = 3, 32
     streams, fn, base, scale = make(6, P, 1, D)
     fn[:] = 0
-    coll, post, comb = oracle.hc_prepare(streams, 1, D, fn, base, scale, 20, EPS)
-    pre = 1 / (1 + np.exp(-float(base[0]))) + EPS
-    c = 1.0 + EPS                       # softmax of one element, plus eps
-    c = c / (c + EPS)                   # column normalisation
+    coll, post, comb = oracle.hc_prepare(streams, 1, D, fn, base, scale, 20, eps)
+    pre = 1 / (1 + np.exp(-float(base[0]))) + eps
+    c = 1.0 + eps                       # softmax of one element, plus eps
+    c = c / (c + eps)                   # column normalisation
     for _ in range(19):
-        c = c / (c + EPS)
-        c = c / (c + EPS)
+        c = c / (c + eps)
+        c = c / (c + eps)
     assert np.allclose(comb, c, rtol=1e-14) and np.allclose(post, 2 / (1 + np.exp(-float(base[1]))), rtol=1e-14)
     want = (streams.reshape(P, D).view(np.float16).astype(np.float64) * pre).astype(np.float16)
     assert np.array_equal(coll, want.view(np.uint16))
@@ -140,3 +143,52 @@ def test_hc_mix_transpose_and_closed_form(oracle):
     o1 = oracle.hc_mix(b.view(np.uint16), post, comb2, res.view(np.uint16)).view(np.float16)
     o2 = oracle.hc_mix((b * np.float16(2)).view(np.uint16), post, comb2, (res * np.float16(2)).view(np.uint16))
     assert np.array_equal(o2.view(np.float16), o1 * np.float16(2))
+
+
+def sinkhorn_rank1(v, N, iters, eps):
+    """Sinkhorn on a matrix whose N rows all equal v: the column sums are N * v_j and every
+    row sums to sum(v), so the matrix keeps equal rows and the iteration is a recursion on
+    v alone: columns, then (iters - 1) x (rows, columns), each denominator + eps."""
+    v = v / (N * v + eps)
+    for _ in range(iters - 1):
+        v = v / (v.sum() + eps)
+        v = v / (N * v + eps)
+    return v
+
+
+@pytest.mark.parametrize("eps", [EPS, 1e-3, 0.05])
+@pytest.mark.parametrize("iters", [1, 2, 3, 20])
+def test_sinkhorn_equal_rows_closed_form(oracle, eps, iters):
+    # fn = 0, so the comb logits are base[2N + i*N + j]: make them vary along j only. The
+    # softmax over j gives every row the same v = softmax(a) + eps, and Sinkhorn reduces to
+    # the recursion above. At iters = 1 (columns only) the entries are ~1/N; normalising
+    # rows first would leave them ~softmax(a). Each eps is visible at eps >= 1e-3, and each
+    # iteration changes v by more than the tolerance while it is far from 1/N.
+    N, D = 4, 32
+    streams, fn, base, scale = make(9, 2, N, D)
+    fn[:] = 0
+    a = np.array([1.7, -0.9, 0.4, -2.2], np.float32)
+    base[2 * N:] = np.tile(a, N)
+    _, _, comb = oracle.hc_prepare(streams, N, D, fn, base, scale, iters, eps)
+    z = a.astype(np.float64)
+    v = np.exp(z - z.max())
+    v = v / v.sum() + eps
+    want = sinkhorn_rank1(v, N, iters, eps)
+    assert np.allclose(comb, np.broadcast_to(want, comb.shape), rtol=1e-13, atol=0)
+
+
+def test_sinkhorn_iteration_count_is_load_bearing(oracle):
+    # softmax + eps matrices from logits spread over [-3, 3] (the reference hc_test's
+    # kind 1): one iteration leaves the row sums far from 1, 3 and 4 iterations differ,
+    # and 20 leave the columns at 1 (the last step) and the rows much closer to 1 than 4
+    # do (how close depends on the matrix: 8e-4 for this one, 1e-6 after 100)
+    N, D, P = 4, 32, 2
+    streams, fn, base, scale = make(10, P, N, D)
+    fn[:] = 0
+    base[2 * N:] = np.random.default_rng(11).uniform(-3, 3, size=N * N).astype(np.float32)
+    out = {k: oracle.hc_prepare(streams, N, D, fn, base, scale, k, EPS)[2] for k in (1, 3, 4, 20)}
+    assert np.max(np.abs(out[1].sum(2) - 1)) > 1e-3
+    assert np.max(np.abs(out[3] - out[4])) > 1e-4
+    assert np.max(np.abs(out[20].sum(1) - 1)) <= 1e-5
+    rows4, rows20 = (np.max(np.abs(out[k].sum(2) - 1)) for k in (4, 20))
+    assert rows20 <= 1e-3 and rows20 < rows4 / 10
