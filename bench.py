@@ -20,6 +20,13 @@ mcg shared expert, 8 hot experts taking about a quarter of the selections), smal
 (configs[0]: hidden 512, 16 experts, top-2, K4 mcg, one row) or trellis_linear
 (configs[1]).
 
+Clock settle: before its W warmup steps, each run keeps the GPU busy with untimed
+steps of the same workload for --settle-ms (default 300 ms; reported in the line as
+`settle`). MI355X raises its clocks over the first ~100-200 ms of sustained load: at
+W=5 and K=20 right after the layers are built, a B=8 step measured ~0.14 ms, against
+~0.12 ms for the same 20 steps once the clocks have settled. The timed region is still
+exactly K full steps.
+
 Output: one JSON line. `value` = 8 rows / (wall time per step) with inputs resident in
 HBM. `roofline` = the routed gate|up kernel (the dominant kernel): algorithmic trellis
 bytes of the distinct experts it streams per launch / its average launch time (HIP
@@ -43,6 +50,22 @@ sys.path.insert(0, os.path.join(ROOT, "exl3-server_amd"))
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix peak
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_glm5_b8_traffic.md")
+
+
+def settle(step, ms):
+    """Untimed steps of the workload until `ms` of wall time has passed (checked every 16
+    steps, each check waits for the GPU): the clocks reach their sustained level before
+    the warmup and the timed steps. Returns {"ms": elapsed, "steps": steps run}."""
+    import torch
+    n, t0 = 0, time.perf_counter()
+    while ms > 0:
+        for _ in range(16):
+            step(n)
+            n += 1
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= ms:
+            break
+    return {"ms": round((time.perf_counter() - t0) * 1e3, 1), "steps": n}
 
 
 def measured_traffic(kernel):
@@ -88,7 +111,7 @@ def bench_linear(args):
 
     dev = torch.device("cuda:0")
 
-    def run(in_f, out_f, K, steps, warmup, cb=1):
+    def run(in_f, out_f, K, steps, warmup, cb=1, settle_ms=50.0):
         nbytes = in_f * out_f // 256 * 32 * K
         copies = max(2, -(-(512 << 20) // nbytes))
         su = f16_from_bits(synth.normal_f16(1, "lin.suh", (in_f,), 1.0, 0.05), dev)
@@ -106,6 +129,7 @@ def bench_linear(args):
         def step(i):
             call("exl3_trellis_linear", C.byref(descs[i % copies]), x.data_ptr(), 1, y.data_ptr(),
                  wsb.data_ptr(), wsb.numel(), st)
+        settled = settle(step, min(settle_ms, args.settle_ms))
         for i in range(warmup):
             step(i)
         torch.cuda.synchronize()
@@ -118,11 +142,13 @@ def bench_linear(args):
         ms = e0.elapsed_time(e1) / steps
         del ws
         torch.cuda.empty_cache()
+        run.settled = settled
         return ms, nbytes / (ms * 1e-3) / 1e9
 
     steps = args.steps if args.steps is not None else 400
     warmup = args.warmup if args.warmup is not None else 40
-    ms, gbps = run(4096, 24576, 4, steps, warmup)
+    ms, gbps = run(4096, 24576, 4, steps, warmup, settle_ms=args.settle_ms)
+    settled = run.settled
     # the reference's headline tensor classes (tests/glm5_gemv_nt_test.cpp:147-171) at rows = 1
     classes = {}
     for name, (i_f, o_f, K, cb) in (("lm_head 4096x154880 K6 mcg", (4096, 154880, 6, 1)),
@@ -140,7 +166,8 @@ def bench_linear(args):
             sweep[f"{name}_K{K}"] = {"ms": round(kms, 5), "GBps": round(kg, 1)}
     line = {
         "metric": "trellis linear GB/s on trellis bytes, rows=1, 1 MI355X", "value": round(gbps, 1),
-        "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
+        "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "settle": settled,
+        "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic",
         "config": {"workload": "trellis_linear", "in": 4096, "out": 24576, "K": 4, "codebook": "mcg",
@@ -196,7 +223,10 @@ def bench_block(args):
         li = i % n_layers
         layers[li][2](xs[li], out=ys[li], ws=wss[li])
 
+    settled = []
+
     def timed(fn):
+        settled.append(settle(fn, args.settle_ms if not settled else min(50.0, args.settle_ms)))
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
@@ -213,6 +243,7 @@ def bench_block(args):
     line = {
         "metric": "MoE MLP sub-block tokens/s (hc prepare + RMSNorm + MoE + hc mix), B=8, 1 MI355X",
         "value": round(B / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "settle": settled[0],
         "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic",
         "config": {"workload": "glm5_moe_block_b8", "batch": B, "hidden": H, "hc_mult": NS, "sinkhorn_iters": 20,
@@ -400,6 +431,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=None, help="default 40 (prefill: 3)")
     ap.add_argument("--layers", type=int, default=None,
                     help="distinct layer instances rotated (default 8; prefill: 2)")
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="untimed steps of the workload for this long before the warmup, so "
+                         "that the GPU clocks settle (0: none)")
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -443,6 +477,7 @@ def main():
         li = i % args.layers
         layers[li][2](xs[li], out=outs[li], ws=wss[li])
 
+    settled = settle(step, args.settle_ms)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -505,7 +540,7 @@ def main():
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": args.warmup, "settle": settled,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",

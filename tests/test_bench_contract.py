@@ -1,6 +1,6 @@
 """bench.py's output contract: one JSON line whose keys the round driver reads (metric,
 value, unit, n_gpus, steps, warmup, ms_per_step, higher_is_better, scaling,
-vs_baseline, dtype, data, config, roofline, cpu_baseline), the metric named as in
+vs_baseline, dtype, data, config, roofline, cpu_baseline, settle), the metric named as in
 BASELINE.json, and a refusal with exit status 2 for more than one GPU. The GPU case
 runs bench.py as a child process at a few steps."""
 import json
@@ -57,8 +57,10 @@ def test_bench_line_small_and_metric_workload():
                   "--no-cpu-baseline")
     check_line(d, 5, 2, 1)
     assert d["config"]["workload"] == "small_b1" and d["cpu_baseline"] is None
-    d = run_bench("--steps", "5", "--warmup", "2", "--layers", "1", "--no-cpu-baseline")
+    d = run_bench("--steps", "5", "--warmup", "2", "--layers", "1", "--no-cpu-baseline", "--settle-ms", "20")
     check_line(d, 5, 2, 8)
+    # the clock-settle phase ran untimed steps for at least the requested time
+    assert d["settle"]["ms"] >= 20 and d["settle"]["steps"] >= 16
     with open(os.path.join(ROOT, "BASELINE.json")) as f:
         assert d["metric"] == json.load(f)["metric"]
     assert d["config"]["workload"] == "glm5_moe_decode_b8" and d["config"]["batch"] == 8
