@@ -39,6 +39,12 @@ __device__ __forceinline__ float f32_rounded(float v) {
 __device__ __forceinline__ f16 to_f16(float v) { return (f16)f32_rounded(v); }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)bitcast<f16>(h); }
 __device__ __forceinline__ uint16_t f32_to_f16(float v) { return bitcast<uint16_t>(to_f16(v)); }
+// Two f32 values rounded to f16 and packed (a in the low half): one v_cvt_pk_f16_f32 on
+// gfx950 (round to nearest even, as v_cvt_f16_f32), in place of two conversions and an or.
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  const f16x2 v = {to_f16(a), to_f16(b)};
+  return bitcast<uint32_t>(v);
+}
 
 // ---------------------------------------------------------------------------------
 // Procedural codebooks (reference exl3.cpp:21-42; GPU form trellis_gemm.cpp:333-356).

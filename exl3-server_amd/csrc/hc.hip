@@ -142,7 +142,7 @@ __device__ __forceinline__ void rms_pairs(const float (&x0)[kHcPairs], const flo
     if (pair_d(i) < D) {
       const float n0 = (float)to_f16(x0[i] * r), n1 = (float)to_f16(x1[i] * r);
       *reinterpret_cast<uint32_t *>(y + pair_d(i)) =
-          (uint32_t)f32_to_f16(n0 * h2f(wv[i] & 0xffff)) | ((uint32_t)f32_to_f16(n1 * h2f(wv[i] >> 16)) << 16);
+          pack_f16x2(n0 * h2f(wv[i] & 0xffff), n1 * h2f(wv[i] >> 16));
     }
 }
 
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
     for (int i = 0; i < kHcPairs; ++i)
       if (pair_d(i) < D)
         *reinterpret_cast<uint32_t *>(out + p * D + pair_d(i)) =
-            (uint32_t)f32_to_f16(x0[i]) | ((uint32_t)f32_to_f16(x1[i]) << 16);
+            pack_f16x2(x0[i], x1[i]);
     return;
   }
   rms_pairs(x0, x1, D, norm_eps, wv, out + p * D, red);

@@ -778,8 +778,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     r0 += rf16(d0);
     r1 += rf16(d1);
   }
-  const uint32_t o = (uint32_t)bitcast<uint16_t>(to_f16(r0)) |
-                     ((uint32_t)bitcast<uint16_t>(to_f16(r1)) << 16);
+  const uint32_t o = pack_f16x2(r0, r1);
   *reinterpret_cast<uint32_t *>(a.out + (int64_t)row * a.H + c) = o;
   if (a.hc_out) {
     // the hyper-connection mix behind the layer (g5_hc_mix), on the f16 output

@@ -45,9 +45,7 @@ namespace {
 
 __device__ __forceinline__ float lo16(uint32_t v) { return (float)bitcast<f16>((uint16_t)(v & 0xffffu)); }
 __device__ __forceinline__ float hi16(uint32_t v) { return (float)bitcast<f16>((uint16_t)(v >> 16)); }
-__device__ __forceinline__ uint32_t pack16(float a, float b) {
-  return (uint32_t)bitcast<uint16_t>(to_f16(a)) | ((uint32_t)bitcast<uint16_t>(to_f16(b)) << 16);
-}
+__device__ __forceinline__ uint32_t pack16(float a, float b) { return pack_f16x2(a, b); }
 __device__ __forceinline__ float rf16(float v) { return (float)to_f16(v); }
 
 // A value every lane of the wave holds (a workgroup's run record, a staged row index),

@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256) void k_qmv(exl3h::PtrTable trellis, int tiles_
           float v0 = f16_to_f32((uint16_t)(hx[q] & 0xffffu)), v1 = f16_to_f32((uint16_t)(hx[q] >> 16));
           wave_had_pre(v0, v1, f16_to_f32((uint16_t)(sx[q] & 0xffffu)), f16_to_f32((uint16_t)(sx[q] >> 16)));
           stage_pair<kDup>(xs + (bi >> nblk_lg) * xs_stride, bi & (nblk - 1), lane,
-                           (uint32_t)f32_to_f16(v0) | ((uint32_t)f32_to_f16(v1) << 16));
+                           pack_f16x2(v0, v1));
         }
       }
     }
