@@ -709,7 +709,14 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     for (int j = 0; j < kCombineBatch; ++j) svp[j] = a.svh_s[2] + (int64_t)e[j] * a.H;
     uint32_t sv[kCombineBatch];
     float2 y[kCombineBatch];
-    if (n_sl <= kCombineSlices) {
+    if (n_sl == 1) {
+      // long-run calls: one folded partial per slot
+#pragma unroll
+      for (int j = 0; j < kCombineBatch; ++j) {
+        sv[j] = *reinterpret_cast<const uint32_t *>(svp[j] + c);
+        y[j] = *reinterpret_cast<const float2 *>(a.yhat_dn + slot[j] * a.S_dn * plane + c);
+      }
+    } else if (n_sl <= kCombineSlices) {
       float2 part[kCombineBatch][kCombineSlices];
 #pragma unroll
       for (int j = 0; j < kCombineBatch; ++j) {

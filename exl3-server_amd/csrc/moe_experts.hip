@@ -510,11 +510,17 @@ __global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_m
   const float *pg = a.yhat_gu + (slot * 2 + 0) * gu_stride * a.Imax + c;
   const float *pu = a.yhat_gu + (slot * 2 + 1) * gu_stride * a.Imax + c;
   float2 vg[kMaxSl], vu[kMaxSl];
+  if (gu_sl == 1) {
+    // long-run calls: the slices are already folded into slice position 0
+    vg[0] = *reinterpret_cast<const float2 *>(pg);
+    vu[0] = *reinterpret_cast<const float2 *>(pu);
+  } else {
 #pragma unroll
-  for (int q = 0; q < kMaxSl; ++q) {
-    const int64_t o = (int64_t)min(q, gu_sl - 1) * a.Imax;
-    vg[q] = *reinterpret_cast<const float2 *>(pg + o);
-    vu[q] = *reinterpret_cast<const float2 *>(pu + o);
+    for (int q = 0; q < kMaxSl; ++q) {
+      const int64_t o = (int64_t)min(q, gu_sl - 1) * a.Imax;
+      vg[q] = *reinterpret_cast<const float2 *>(pg + o);
+      vu[q] = *reinterpret_cast<const float2 *>(pu + o);
+    }
   }
   const int e = shared_mode ? a.E : a.slot_e[slot];
   const int64_t so = (int64_t)e * a.Imax;
