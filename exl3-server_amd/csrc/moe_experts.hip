@@ -257,7 +257,11 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kDnW
 using exl3m::kLongBlocks;
 using exl3m::kLongRows;
 constexpr int kLongThreads = 512;
-constexpr int kStageBatch = 4;  // staging loads in flight per lane
+// Staging loads in flight per lane: gate/up stages a 4-step part of duplicated rows,
+// 48 rows x 32 chunks = 3 chunks per thread (one round); down a slice of plain rows,
+// 48 x 64 = 6 per thread (two rounds of 4, the last two clamped copies).
+constexpr int kStageBatchGu = 3;
+constexpr int kStageBatchDn = 4;
 
 // Work unit u of the long-run kernels: pass u of the dispatch's pass table, or (shared
 // mode) rows [u * kLongRows, u * kLongRows + kLongRows) of the trellis shared expert.
@@ -327,16 +331,16 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
         // this projection, in the staged k order)
         const int k0 = (sl * n_parts + pt) * part_k;
         const int items = nr * q_row;
-        for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatch) {
-          uint4 c[kStageBatch];
+        for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatchGu) {
+          uint4 c[kStageBatchGu];
 #pragma unroll
-          for (int q = 0; q < kStageBatch; ++q) {
+          for (int q = 0; q < kStageBatchGu; ++q) {
             const int i = min(i0 + q * kLongThreads, items - 1);
             c[q] = reinterpret_cast<const uint4 *>(
                 a.xrot + ((int64_t)(ri.off + p0 + (i >> q_lg)) * 2 + proj) * a.H + k0)[i & (q_row - 1)];
           }
 #pragma unroll
-          for (int q = 0; q < kStageBatch; ++q) {
+          for (int q = 0; q < kStageBatchGu; ++q) {
             const int i = i0 + q * kLongThreads;
             if (i < items) stage_chunk<kDup>(xs + (i >> q_lg) * xs_stride, i & (q_row - 1), c[q]);
           }
@@ -401,16 +405,16 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
       for (int pt = 0; pt < n_parts; ++pt) {
         const int k0 = (sl * n_parts + pt) * part_k;
         const int items = nr * q_row;  // 16-byte chunks of the part's rows
-        for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatch) {
-          uint4 c[kStageBatch];
+        for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatchDn) {
+          uint4 c[kStageBatchDn];
 #pragma unroll
-          for (int q = 0; q < kStageBatch; ++q) {
+          for (int q = 0; q < kStageBatchDn; ++q) {
             const int i = min(i0 + q * kLongThreads, items - 1);
             c[q] = reinterpret_cast<const uint4 *>(a.act + (int64_t)(ri.off + p0 + (i >> q_lg)) * a.Imax +
                                                    k0)[i & (q_row - 1)];
           }
 #pragma unroll
-          for (int q = 0; q < kStageBatch; ++q) {
+          for (int q = 0; q < kStageBatchDn; ++q) {
             const int i = i0 + q * kLongThreads;
             if (i < items) stage_chunk<kDup>(xs + (i >> q_lg) * xs_stride, i & (q_row - 1), c[q]);
           }
