@@ -491,6 +491,64 @@ __global__ __launch_bounds__(256) void k_moe_rotate(MoeArgs a, int n_slots) {
 // the MFMA k order the down kernel stages). Routed slots come from the dispatch; in
 // shared mode the slots P..P+N-1 of the trellis shared expert.
 constexpr int kActThreads = 256;
+constexpr int kActBatch = 4;  // (slot, block) items per wave of a long-run call
+
+// Long-run calls (the gate/up slices already folded at slice position 0): a wave takes
+// kActBatch consecutive (slot, block) items, issues all their loads before the first
+// Hadamard and runs their rotations together; per item the arithmetic is k_moe_act's.
+__device__ __forceinline__ void act_folded(const MoeArgs &a, int shared_mode, int64_t g0,
+                                           int64_t n_items, int nblk) {
+  const int lane = threadIdx.x & 63;
+  const int gu_stride = n_slices(a.H / 16);
+  int64_t slot[kActBatch];
+  int blk[kActBatch], e[kActBatch];
+  float2 vg[kActBatch], vu[kActBatch];
+#pragma unroll
+  for (int j = 0; j < kActBatch; ++j) {
+    const int64_t item = min(g0 + j, n_items - 1);
+    blk[j] = (int)(item % nblk);
+    slot[j] = (shared_mode ? a.P : 0) + item / nblk;
+    const int c = blk[j] * 128 + 2 * lane;
+    vg[j] = *reinterpret_cast<const float2 *>(a.yhat_gu + (slot[j] * 2 + 0) * gu_stride * a.Imax + c);
+    vu[j] = *reinterpret_cast<const float2 *>(a.yhat_gu + (slot[j] * 2 + 1) * gu_stride * a.Imax + c);
+    e[j] = shared_mode ? a.E : a.slot_e[slot[j]];
+  }
+  uint32_t svg[kActBatch], svu[kActBatch], sud[kActBatch];
+#pragma unroll
+  for (int j = 0; j < kActBatch; ++j) {
+    const int64_t so = (int64_t)e[j] * a.Imax + blk[j] * 128 + 2 * lane;
+    svg[j] = *reinterpret_cast<const uint32_t *>(a.svh_s[0] + so);
+    svu[j] = *reinterpret_cast<const uint32_t *>(a.svh_s[1] + so);
+    sud[j] = *reinterpret_cast<const uint32_t *>(a.suh_s[2] + so);
+  }
+  float y0[2 * kActBatch], y1[2 * kActBatch], s0[2 * kActBatch], s1[2 * kActBatch];
+#pragma unroll
+  for (int j = 0; j < kActBatch; ++j) {
+    y0[2 * j] = vg[j].x;
+    y1[2 * j] = vg[j].y;
+    y0[2 * j + 1] = vu[j].x;
+    y1[2 * j + 1] = vu[j].y;
+    s0[2 * j] = lo16(svg[j]);
+    s1[2 * j] = hi16(svg[j]);
+    s0[2 * j + 1] = lo16(svu[j]);
+    s1[2 * j + 1] = hi16(svu[j]);
+  }
+  wave_had_post_n<2 * kActBatch>(y0, y1, s0, s1);
+  const float L = rf16(a.swiglu_limit);
+  float a0[kActBatch], a1[kActBatch], d0[kActBatch], d1[kActBatch];
+#pragma unroll
+  for (int j = 0; j < kActBatch; ++j) {
+    a0[j] = swiglu1(rf16(y0[2 * j]), rf16(y0[2 * j + 1]), L);
+    a1[j] = swiglu1(rf16(y1[2 * j]), rf16(y1[2 * j + 1]), L);
+    d0[j] = lo16(sud[j]);
+    d1[j] = hi16(sud[j]);
+  }
+  wave_had_pre_n<kActBatch>(a0, a1, d0, d1);
+#pragma unroll
+  for (int j = 0; j < kActBatch; ++j)
+    if (g0 + j < n_items)
+      stage_pair<false>(reinterpret_cast<uint32_t *>(a.act + slot[j] * a.Imax), blk[j], lane, pack16(a0[j], a1[j]));
+}
 
 __global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_mode, int dense_blocks) {
   if ((int)blockIdx.x < dense_blocks) {
@@ -502,6 +560,11 @@ __global__ __launch_bounds__(kActThreads) void k_moe_act(MoeArgs a, int shared_m
   const int nblk = in / 128;
   const int64_t gw = (int64_t)(blockIdx.x - dense_blocks) * (kActThreads / 64) + (threadIdx.x >> 6);
   const int n_slots = shared_mode ? a.N : a.P;
+  if (a.fold) {
+    const int64_t n_items = (int64_t)n_slots * nblk;
+    if (gw * kActBatch < n_items) act_folded(a, shared_mode, gw * kActBatch, n_items, nblk);
+    return;
+  }
   if (gw >= (int64_t)n_slots * nblk) return;
   const int blk = (int)(gw % nblk);
   const int64_t slot = (shared_mode ? a.P : 0) + gw / nblk;
@@ -714,7 +777,8 @@ exl3_status launch_moe_rotate(const MoeArgs &a, bool shared_trellis, hipStream_t
 // activations, after `dense_blocks` workgroups of the f16 shared expert's SwiGLU.
 exl3_status launch_moe_act(const MoeArgs &a, int shared_mode, int dense_blocks, hipStream_t st) {
   const int in = shared_mode ? a.SI : a.I;
-  const int64_t waves = (int64_t)(shared_mode ? a.N : a.P) * (in / 128);
+  int64_t waves = (int64_t)(shared_mode ? a.N : a.P) * (in / 128);
+  if (a.fold) waves = (waves + kActBatch - 1) / kActBatch;  // kActBatch items per wave
   const unsigned blocks = (unsigned)((waves + 3) / 4) + (unsigned)dense_blocks;
   if (blocks == 0) return EXL3_OK;
   k_moe_act<<<blocks, kActThreads, 0, st>>>(a, shared_mode, dense_blocks);
