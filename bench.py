@@ -171,7 +171,7 @@ def bench_linear(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic",
         "config": {"workload": "trellis_linear", "in": 4096, "out": 24576, "K": 4, "codebook": "mcg",
-                   "rows": 1, "parallelism": "none (one GPU)"},
+                   "rows": 1, "weight_form": args.weight_form, "parallelism": "none (one GPU)"},
         "roofline": {"kernel": "exl3_trellis_linear (QMV with the input Hadamard, finalize)", "bound": "hbm",
                      "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
@@ -200,6 +200,8 @@ def bench_block(args):
     n_layers = args.layers if args.layers is not None else 8
     dev = torch.device("cuda:0")
     cfg, layers = build_layers(n_layers, args.seed, dev, "glm5")
+    for _, _, d in layers:
+        d.set_tuning(weight_form=1 if args.weight_form == "halves" else 0)
     H, B, NS = cfg.hidden, 8, 4
     rng = np.random.default_rng(args.seed)
     W = (2 + NS) * NS
@@ -437,6 +439,9 @@ def main():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--weight-form", choices=("reference", "halves"), default="reference",
+                    help="mcg/3inst GEMV weights: the reference's f16 values (default) or the "
+                         "opt-in exact halves (exl3_tuning.weight_form)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed steps, run one plain device copy of 256 MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -452,6 +457,9 @@ def main():
     from exl3_amd import synth
 
     kind, B, _ = WORKLOADS[args.workload]
+    form = 1 if args.weight_form == "halves" else 0
+    from exl3_amd.trellis import trellis_set_tuning
+    trellis_set_tuning(weight_form=form)
     if kind == "linear":
         bench_linear(args)
         return
@@ -465,6 +473,8 @@ def main():
     dev = torch.device("cuda:0")
     t0 = time.time()
     cfg, layers = build_layers(args.layers, args.seed, dev, kind)
+    for _, _, d in layers:
+        d.set_tuning(weight_form=form)
     H = cfg.hidden
     xs = [torch.from_numpy(make_inputs(args.workload, args.seed, li, B, H).view(np.float16))
           .to(dev).view(B, 1, H) for li in range(args.layers)]
@@ -551,7 +561,8 @@ def main():
                    "moe_intermediate": cfg.inter, "experts": cfg.n_experts, "top_k": cfg.top_k,
                    "gate_up": f"K{cfg.gate_up_K} {cbn[cfg.gate_up_cb]}",
                    "down": f"K{cfg.down_K} {cbn[cfg.down_cb]}", "shared_expert": shared,
-                   "layer_instances": args.layers, "parallelism": "none (one GPU)"},
+                   "layer_instances": args.layers, "weight_form": args.weight_form,
+                   "parallelism": "none (one GPU)"},
         "roofline": {"kernel": "k_moe_gate_up", "bound": "hbm", "achieved": round(gu_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic("k_moe_gate_up") if args.workload == "glm5_moe_decode_b8" else None,

@@ -26,11 +26,18 @@ exl3_status hip_check(hipError_t e, const char *what) {
 }
 
 static std::mutex g_tuning_mu;
-static exl3_tuning g_tuning = {0, 16, 0};
+static exl3_tuning g_tuning = {0, 16, 0, EXL3_FORM_REFERENCE};
 
 exl3_tuning tuning() {
   std::lock_guard<std::mutex> lk(g_tuning_mu);
   return g_tuning;
+}
+
+exl3_status check_tuning(const exl3_tuning *t) {
+  if (!t) return fail(EXL3_ERR_INVALID, "null tuning");
+  if (t->weight_form != EXL3_FORM_REFERENCE && t->weight_form != EXL3_FORM_HALVES)
+    return fail(EXL3_ERR_INVALID, "weight_form must be EXL3_FORM_REFERENCE or EXL3_FORM_HALVES");
+  return EXL3_OK;
 }
 
 exl3_status check_desc(const exl3_trellis_desc *w, bool need_128) {
@@ -122,10 +129,11 @@ extern "C" {
 
 const char *exl3_last_error(void) { return g_last_error.c_str(); }
 
-int32_t exl3_abi_version(void) { return 1; }
+int32_t exl3_abi_version(void) { return 2; }
 
 exl3_status exl3_set_tuning(const exl3_tuning *t) {
-  if (!t) return fail(EXL3_ERR_INVALID, "null tuning");
+  exl3_status rc = check_tuning(t);
+  if (rc) return rc;
   std::lock_guard<std::mutex> lk(g_tuning_mu);
   g_tuning = *t;
   return EXL3_OK;

@@ -39,8 +39,9 @@ int qmv_slices(int in);
 // Token rows per MFMA pass of the standalone/grouped linear (rows_per_pass knob, <= 16).
 int qmv_pass_rows(int64_t rows);
 
-// Scheduling knobs (exl3_set_tuning).
+// Scheduling knobs (exl3_set_tuning) and their validation.
 exl3_tuning tuning();
+exl3_status check_tuning(const exl3_tuning *t);
 
 // Validates a trellis descriptor for the Hadamard-based paths.
 exl3_status check_desc(const exl3_trellis_desc *w, bool need_128);

@@ -850,7 +850,7 @@ struct exl3_moe_layer_s {
   size_t scale_off[6]; // suh 0..2, svh 0..2 (f16 elements)
   std::vector<int64_t> expert_bytes;  // trellis bytes of gate + up + down per routed expert
   std::vector<int64_t> gu_bytes, dn_bytes;  // trellis bytes of gate+up / down per expert
-  exl3_tuning tuning;  // this handle's staged-path window (the diag's staged runs)
+  exl3_tuning tuning;  // the handle's knobs: staged-path window (diag), weight form
   std::vector<void *> owned;           // device buffers of a loaded layer (exl3_moe_layer_load)
   int64_t loaded_in_place = 0, loaded_repacked = 0;
   int diag_on;
@@ -1414,11 +1414,13 @@ bool side_stream_on() {
 exl3_status launch_shared_trellis(const exl3_moe_layer_s *layer, const MoeArgs &a, int64_t N,
                                   hipStream_t st) {
   const int64_t sh_units = a.fold ? (N + kLongRows - 1) / kLongRows : 1;
-  exl3_status rc = launch_moe_expert(0, layer->sh_K, layer->sh_cb, sh_units, a, 1, false, st);
+  exl3_status rc = launch_moe_expert(0, layer->sh_K, kernel_cb(layer->sh_cb, a.weight_form), sh_units, a, 1,
+                                     false, st);
   if (rc) return rc;
   rc = launch_moe_act(a, 1, 0, st);
   if (rc) return rc;
-  return launch_moe_expert(1, layer->sh_dn_K, layer->sh_dn_cb, sh_units, a, 1, false, st);
+  return launch_moe_expert(1, layer->sh_dn_K, kernel_cb(layer->sh_dn_cb, a.weight_form), sh_units, a, 1,
+                           false, st);
 }
 }  // namespace
 
@@ -1629,6 +1631,11 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
   exl3_status rc = EXL3_OK;
   hipStream_t st = stream_of(stream);
   MoeArgs a = make_args(layer, m, N, h, out, (char *)workspace);
+  {
+    // the handle's weight form, read once per call
+    std::lock_guard<std::mutex> lk(layer->mu);
+    a.weight_form = layer->tuning.weight_form;
+  }
   if (epi) {
     a.hc_n = epi->n;
     a.hc_post = epi->post;
@@ -1684,9 +1691,13 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
       join_side(true);
       return rc;
     }
-    EXL3_HIP(hipEventRecord(layer->join, layer->side));
+    const hipError_t e = hipEventRecord(layer->join, layer->side);
+    if (e != hipSuccess) {
+      join_side(true);
+      return hip_check(e, "hipEventRecord(join)");
+    }
   }
-  rc = launch_moe_expert(0, layer->gu_K, layer->gu_cb, units, a, 0, dense_sh, st);
+  rc = launch_moe_expert(0, layer->gu_K, kernel_cb(layer->gu_cb, a.weight_form), units, a, 0, dense_sh, st);
   if (rc) return fail_joined(rc);
   if (timed) {
     const hipError_t e = hipEventRecord(layer->ev[2], st);
@@ -1696,7 +1707,7 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
   // (+ the f16 shared expert's down partials)
   rc = launch_moe_act(a, 0, dense_sh ? shared_swiglu_blocks(N, layer->SI) : 0, st);
   if (rc) return fail_joined(rc);
-  rc = launch_moe_expert(1, layer->dn_K, layer->dn_cb, units, a, 0, dense_sh, st);
+  rc = launch_moe_expert(1, layer->dn_K, kernel_cb(layer->dn_cb, a.weight_form), units, a, 0, dense_sh, st);
   if (rc) return fail_joined(rc);
   if (timed) {
     const hipError_t e = hipEventRecord(layer->ev[3], st);
@@ -1704,8 +1715,9 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
   }
   // a trellis shared expert: one run of every token row through the same kernels
   if (side) {
+    const hipError_t e = hipStreamWaitEvent(st, layer->join, 0);
+    if (e != hipSuccess) return fail_joined(hip_check(e, "hipStreamWaitEvent(join)"));
     forked = false;
-    EXL3_HIP(hipStreamWaitEvent(st, layer->join, 0));
   } else if (layer->shared == exl3m::kSharedTrellis) {
     rc = launch_shared_trellis(layer, a, N, st);
     if (rc) return rc;
@@ -1785,7 +1797,9 @@ exl3_status exl3_moe_layer_load_info(exl3_moe_layer_t layer, int64_t *in_place, 
 }
 
 exl3_status exl3_moe_set_tuning(exl3_moe_layer_t layer, const exl3_tuning *t) {
-  if (!layer || !t) return fail(EXL3_ERR_INVALID, "null argument");
+  if (!layer) return fail(EXL3_ERR_INVALID, "null argument");
+  exl3_status rc = check_tuning(t);
+  if (rc) return rc;
   std::lock_guard<std::mutex> lk(layer->mu);
   layer->tuning = *t;
   return EXL3_OK;

@@ -73,6 +73,7 @@ struct MoeArgs {
   int xrot_rows;      // 1: the short-run gate/up kernel copies the rows k_moe_rotate rotated
   int gu_items;       // 128-column blocks per short-run gate/up workgroup (one k slice)
   int dn_items;       // 128-column blocks per short-run down workgroup
+  int weight_form;    // host side: the call's exl3_weight_form (the kernel codebooks)
   // inputs
   const uint16_t *h;          // (N, H) f16
   const uint16_t *router_w;   // (E, H) f16

@@ -704,7 +704,8 @@ static int moe_prefetch(int k_tiles, int K) {
 }
 
 // which: 0 = gate/up, 1 = down, over `runs` runs (routed: the dispatch's run table,
-// bounded by R; shared_mode 1: the one trellis-shared run). dense: prepend the f16
+// bounded by R; shared_mode 1: the one trellis-shared run). cb is the kernel codebook
+// (kernel_cb: the tensor codebook under the handle's weight form). dense: prepend the f16
 // shared expert's workgroups for this projection (short-run kernels: whole z planes of
 // the 3-D grid, the workgroups past the shared expert's tasks return at once).
 exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeArgs &a,
@@ -748,9 +749,14 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
   exl3_status rc = EXL3_OK;
 #define EXL3_KC(KK)                                                                            \
   case KK:                                                                                     \
-    if (cb == 0) rc = moe_pd<KK, 0>(pd, which, ub, st, a, shared_mode, dense_arg);         \
-    else if (cb == 1) rc = moe_pd<KK, 1>(pd, which, ub, st, a, shared_mode, dense_arg);    \
-    else rc = moe_pd<KK, 2>(pd, which, ub, st, a, shared_mode, dense_arg);                 \
+    switch (cb) {                                                                              \
+      case 0: rc = moe_pd<KK, 0>(pd, which, ub, st, a, shared_mode, dense_arg); break;        \
+      case 1: rc = moe_pd<KK, 1>(pd, which, ub, st, a, shared_mode, dense_arg); break;        \
+      case 2: rc = moe_pd<KK, 2>(pd, which, ub, st, a, shared_mode, dense_arg); break;        \
+      case 3: rc = moe_pd<KK, 3>(pd, which, ub, st, a, shared_mode, dense_arg); break;        \
+      case 4: rc = moe_pd<KK, 4>(pd, which, ub, st, a, shared_mode, dense_arg); break;        \
+      default: return fail(EXL3_ERR_INVALID, "kernel codebook out of range");                 \
+    }                                                                                          \
     break;
   switch (K) {
     EXL3_KC(1) EXL3_KC(2) EXL3_KC(3) EXL3_KC(4) EXL3_KC(5) EXL3_KC(6) EXL3_KC(7) EXL3_KC(8)

@@ -12,25 +12,27 @@
 // registers with no shuffle. The A operand's 16 rows are 16 token rows staged in LDS
 // in the matching k order: one decode serves up to 16 rows.
 //
-// Two B forms, by codebook:
-//  - mcg, 3inst ("halves"): a weight is the f16 sum of the two f16 halves of its masked
-//    hash word (trellis_gemm.cpp:348-356). The word itself is the B register: its halves
-//    are two k-elements, multiplied by the same activation, so the MFMA forms
-//    x*lo + x*hi in f32 and no VALU add is spent per weight. MFMA (h, j) takes quad
-//    (j, h): 4 words = 8 k-elements. The activations are staged duplicated, each f16
-//    value in both halves of a word. The product is x*(lo + hi) without the f16
-//    rounding of lo + hi (the reconstructed weights of exl3_trellis_decode/reconstruct
-//    are the reference's exact bits; the GEMV differs from a product with those f16
-//    weights by at most 2^-11 of each weight).
-//  - mul1: the weight is one f16 fma (trellis_gemm.cpp:336-345), computed exactly for two
-//    weights per packed register; MFMA (h, jp) takes quads (2jp, h), (2jp+1, h).
+// B forms. The CB template parameter of the GEMV kernels is a kernel codebook: the
+// tensor's codebook in the reference-weight form (0 = 3inst, 1 = mcg, 2 = mul1), or
+// 3 = 3inst, 4 = mcg in the exact-halves form (exl3_tuning.weight_form).
+//  - reference (packed): every weight is the reference's f16 value, two per register;
+//    MFMA (h, jp) takes quads (2jp, h), (2jp+1, h). mcg/3inst: the f16 sum of the two
+//    halves of the masked hash word with one RNE (trellis_gemm.cpp:348-356), written by
+//    v_add_f16 SDWA straight into its half of the operand register; mul1: one f16 fma
+//    (trellis_gemm.cpp:336-345), exact for two weights per packed register.
+//  - halves (mcg, 3inst): the masked word itself is the B register: its halves are two
+//    k-elements, multiplied by the same activation, so the MFMA forms x*lo + x*hi in
+//    f32 and no VALU add is spent per weight. MFMA (h, j) takes quad (j, h): 4 words = 8
+//    k-elements. The activations are staged duplicated, each f16 value in both halves
+//    of a word. The product is x*(lo + hi) without the f16 rounding of lo + hi, so it
+//    differs from the reference's by up to 2^-11 of each weight.
 //
 // Staged activation order in LDS, per token row and k-tile (xpos: f16 pair u = k-rows
 // 2u, 2u+1):
-//  - plain (mul1): 8 words [p0, p4, p1, p5, p2, p6, p3, p7]; words 4jp..4jp+3 are MFMA
-//    jp's A operand. Pair u sits at word xpos(u). This is also the layout of the
-//    rotated activations the MoE kernels keep in HBM (act, xrot).
-//  - duplicated (mcg, 3inst): 16 words, word 2w = (lo, lo) and 2w + 1 = (hi, hi) of
+//  - plain (reference forms): 8 words [p0, p4, p1, p5, p2, p6, p3, p7]; words 4jp..4jp+3
+//    are MFMA jp's A operand. Pair u sits at word xpos(u). This is also the layout of
+//    the rotated activations the MoE kernels keep in HBM (act, xrot).
+//  - duplicated (halves forms): 16 words, word 2w = (lo, lo) and 2w + 1 = (hi, hi) of
 //    plain word w; words 4j..4j+3 are MFMA j's A operand.
 //
 // k partition (a function of the tensor's k-tile count only): the k range is cut
@@ -41,6 +43,7 @@
 #pragma once
 
 #include "exl3_device.hpp"
+#include "exl3_moe.h"
 
 namespace exl3d {
 
@@ -72,8 +75,16 @@ __host__ __device__ constexpr int prefetch_steps(int k_tiles, int K) {
 // Word position of f16 pair u (k-rows 2u, 2u+1) inside a plain staged k-tile.
 __host__ __device__ constexpr int xpos(int u) { return ((u & 3) << 1) | (u >> 2); }
 
-// Staging form of a codebook: duplicated activations for the halves B form.
-__host__ __device__ constexpr bool dup_cb(int cb) { return cb != 2; }
+// Kernel codebooks (see the B forms above).
+constexpr int kHalvesCb = 3;
+// The tensor codebook of kernel codebook kcb.
+__host__ __device__ constexpr int cb_base(int kcb) { return kcb >= kHalvesCb ? kcb - kHalvesCb : kcb; }
+// The kernel codebook of a tensor codebook under a weight form (mul1 has one form).
+__host__ __device__ constexpr int kernel_cb(int cb, int form) {
+  return form == EXL3_FORM_HALVES && cb != 2 ? cb + kHalvesCb : cb;
+}
+// Staging form of a kernel codebook: duplicated activations for the halves B form.
+__host__ __device__ constexpr bool dup_cb(int kcb) { return kcb >= kHalvesCb; }
 // Staged words per token row and k-tile.
 __host__ __device__ constexpr int tile_words(bool dup) { return dup ? 16 : 8; }
 // Staged words per token row of one k slice of a tensor with k_tiles k-tiles.
@@ -101,9 +112,36 @@ __host__ __device__ constexpr int slot_chunks(int K) { return 16 * K > 64 ? 16 *
 // ---------------------------------------------------------------------------------
 // Decode
 // ---------------------------------------------------------------------------------
+// The masked hash word of a state (mcg/3inst): two f16 halves whose sum is the weight.
 template <int CB>
 __device__ __forceinline__ uint32_t cb_bits(uint32_t s) {
-  return (cb_hash<CB>(s) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+  return (cb_hash<cb_base(CB)>(s) & 0x8FFF8FFFu) ^ 0x3B603B60u;
+}
+
+// Eight masked hash words -> the 4-register B operand of one MFMA in the reference
+// form: half i of the operand = f16(m_i.lo + m_i.hi), one RNE, the reference's weight
+// (trellis_gemm.cpp:348-356). Both halves are f16 values of magnitude in [2^-3, 2), so
+// their exact sum is a multiple of 2^-13 and never subnormal. v_add_f16 SDWA writes
+// each sum straight into its half of the operand register (the compiler spells a pair
+// as two funnel shifts, two packed adds and a pack). The compiler's hazard tracking does not
+// see into inline assembly, so the block ends with the wait states a VALU-written VGPR
+// needs before an MFMA reads it.
+__device__ __forceinline__ f16x8 hadd_operand(const uint32_t (&m)[8]) {
+  typedef uint32_t u32x4_ __attribute__((ext_vector_type(4)));
+  uint32_t b0, b1, b2, b3;
+  asm("v_add_f16_sdwa %0, %4, %4 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %1, %6, %6 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %2, %8, %8 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %3, %10, %10 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %0, %5, %5 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %1, %7, %7 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %2, %9, %9 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %3, %11, %11 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "s_nop 1"
+      : "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3)
+      : "v"(m[0]), "v"(m[1]), "v"(m[2]), "v"(m[3]), "v"(m[4]), "v"(m[5]), "v"(m[6]), "v"(m[7]));
+  const u32x4_ v = {b0, b1, b2, b3};
+  return __builtin_bit_cast(f16x8, v);
 }
 
 // mul1: two states -> their f16 weights packed in one register, each one f16 fma
@@ -119,16 +157,25 @@ __device__ __forceinline__ uint32_t mul1_pair(uint32_t s0, uint32_t s1) {
   return bitcast<uint32_t>(__builtin_elementwise_fma(v, inv, bias));
 }
 
-// mul1 B operand of MFMA (h, jp): quads (2jp, h) and (2jp+1, h), i.e. stream positions
-// 16jp + 4h + {0..3} and 16jp + 8 + 4h + {0..3} of this lane's bit string.
-template <int K, int T0>
-__device__ __forceinline__ f16x8 b_mul1(const uint32_t (&W)[K + 1], const uint32_t (&F)[K + 1]) {
-  typedef uint32_t u32x4_ __attribute__((ext_vector_type(4)));
-  const u32x4_ v = {mul1_pair(lane_state<K, T0 + 0>(W, F), lane_state<K, T0 + 1>(W, F)),
-                    mul1_pair(lane_state<K, T0 + 2>(W, F), lane_state<K, T0 + 3>(W, F)),
-                    mul1_pair(lane_state<K, T0 + 8>(W, F), lane_state<K, T0 + 9>(W, F)),
-                    mul1_pair(lane_state<K, T0 + 10>(W, F), lane_state<K, T0 + 11>(W, F))};
-  return __builtin_bit_cast(f16x8, v);
+// Reference-form B operand of MFMA (h, jp): quads (2jp, h) and (2jp+1, h), i.e. stream
+// positions 16jp + 4h + {0..3} and 16jp + 8 + 4h + {0..3} of this lane's bit string
+// (T0 = 16jp + 4h), two f16 weights per register.
+template <int K, int CB, int T0>
+__device__ __forceinline__ f16x8 b_packed(const uint32_t (&W)[K + 1], const uint32_t (&F)[K + 1]) {
+  if constexpr (CB == 2) {
+    typedef uint32_t u32x4_ __attribute__((ext_vector_type(4)));
+    const u32x4_ v = {mul1_pair(lane_state<K, T0 + 0>(W, F), lane_state<K, T0 + 1>(W, F)),
+                      mul1_pair(lane_state<K, T0 + 2>(W, F), lane_state<K, T0 + 3>(W, F)),
+                      mul1_pair(lane_state<K, T0 + 8>(W, F), lane_state<K, T0 + 9>(W, F)),
+                      mul1_pair(lane_state<K, T0 + 10>(W, F), lane_state<K, T0 + 11>(W, F))};
+    return __builtin_bit_cast(f16x8, v);
+  } else {
+    const uint32_t m[8] = {cb_bits<CB>(lane_state<K, T0 + 0>(W, F)),  cb_bits<CB>(lane_state<K, T0 + 1>(W, F)),
+                           cb_bits<CB>(lane_state<K, T0 + 2>(W, F)),  cb_bits<CB>(lane_state<K, T0 + 3>(W, F)),
+                           cb_bits<CB>(lane_state<K, T0 + 8>(W, F)),  cb_bits<CB>(lane_state<K, T0 + 9>(W, F)),
+                           cb_bits<CB>(lane_state<K, T0 + 10>(W, F)), cb_bits<CB>(lane_state<K, T0 + 11>(W, F))};
+    return hadd_operand(m);
+  }
 }
 
 // Halves B operand of MFMA (h, j): the masked hash words of quad (j, h), stream positions
@@ -148,19 +195,19 @@ __device__ __forceinline__ f32x4 mfma16(const f16x8 &a, const f16x8 &b, const f3
 }
 
 // One wave step: this lane's 32 weights into the MFMAs. xa = this lane's staged row at
-// its k-tile of the step; D0/D1 accumulate columns m and m + 8. Halves: 8 MFMAs, j
-// major; mul1: 4 MFMAs, jp major.
+// its k-tile of the step; D0/D1 accumulate columns m and m + 8. Reference forms: 4
+// MFMAs, jp major; halves: 8 MFMAs, j major.
 template <int K, int CB>
 __device__ __forceinline__ void mfma_step(const uint32_t (&W)[K + 1], const uint32_t *xa, f32x4 &D0,
                                           f32x4 &D1) {
   uint32_t F[K + 1];
   lane_funnels<K>(W, F);
-  if constexpr (CB == 2) {
+  if constexpr (!dup_cb(CB)) {
     const f16x8 A0 = lds_a(xa), A1 = lds_a(xa + 4);
-    D0 = mfma16(A0, b_mul1<K, 0>(W, F), D0);
-    D1 = mfma16(A0, b_mul1<K, 4>(W, F), D1);
-    D0 = mfma16(A1, b_mul1<K, 16>(W, F), D0);
-    D1 = mfma16(A1, b_mul1<K, 20>(W, F), D1);
+    D0 = mfma16(A0, b_packed<K, CB, 0>(W, F), D0);
+    D1 = mfma16(A0, b_packed<K, CB, 4>(W, F), D1);
+    D0 = mfma16(A1, b_packed<K, CB, 16>(W, F), D0);
+    D1 = mfma16(A1, b_packed<K, CB, 20>(W, F), D1);
   } else {
     const f16x8 A0 = lds_a(xa), A1 = lds_a(xa + 4);
     D0 = mfma16(A0, b_halves<K, CB, 0>(W, F), D0);
@@ -385,17 +432,17 @@ __device__ __forceinline__ void mfma_step_rb(const uint32_t (&W)[K + 1], const u
                                              const int (&xo)[RB], f32x4 (&D)[RB][2]) {
   uint32_t F[K + 1];
   lane_funnels<K>(W, F);
-  if constexpr (CB == 2) {
+  if constexpr (!dup_cb(CB)) {
     // k-rows 0..7 of the step (A0) before 8..15 (A1), as in mfma_step; two B operands
     // live at a time
-    const f16x8 B0 = b_mul1<K, 0>(W, F), B1 = b_mul1<K, 4>(W, F);
+    const f16x8 B0 = b_packed<K, CB, 0>(W, F), B1 = b_packed<K, CB, 4>(W, F);
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       const f16x8 A0 = lds_a(xs + xo[r]);
       D[r][0] = mfma16(A0, B0, D[r][0]);
       D[r][1] = mfma16(A0, B1, D[r][1]);
     }
-    const f16x8 B2 = b_mul1<K, 16>(W, F), B3 = b_mul1<K, 20>(W, F);
+    const f16x8 B2 = b_packed<K, CB, 16>(W, F), B3 = b_packed<K, CB, 20>(W, F);
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       const f16x8 A1 = lds_a(xs + xo[r] + 4);

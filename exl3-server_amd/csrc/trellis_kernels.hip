@@ -353,7 +353,9 @@ static void qmv_cb(int cb, int pd, dim3 grid, hipStream_t st, const PtrTable &tr
   switch (cb) {
     case 0: qmv_pd<K, 0>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
     case 1: qmv_pd<K, 1>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
-    default: qmv_pd<K, 2>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
+    case 2: qmv_pd<K, 2>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
+    case 3: qmv_pd<K, 3>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
+    default: qmv_pd<K, 4>(pd, grid, st, tr, tiles_n, in, out, xhat, xs, rows, pass_rows, part, suh); break;
   }
 }
 
@@ -376,11 +378,13 @@ exl3_status launch_qmv(const exl3_trellis_desc &shape, const PtrTable &trellis, 
   if (gy > 65535 || n > 65535) return fail(EXL3_ERR_UNSUPPORTED, "linear launch too large");
   dim3 grid((unsigned)(out / 128), (unsigned)gy, (unsigned)n);
   const int tiles_n = out / 16, pd = prefetch_steps(k_tiles, shape.K);
+  // the weight form of the process-wide tuning (the reference's f16 weights by default)
+  const int kcb = kernel_cb(shape.codebook, tuning().weight_form);
   switch (shape.K) {
 #define EXL3_K(KK)                                                                        \
   case KK:                                                                                \
-    qmv_cb<KK>(shape.codebook, pd, grid, st, trellis, tiles_n, in, out, xhat,             \
-               x_member_stride, rows, pr, part, suh);                                     \
+    qmv_cb<KK>(kcb, pd, grid, st, trellis, tiles_n, in, out, xhat, x_member_stride, rows, \
+               pr, part, suh);                                                            \
     break;
     EXL3_K(1) EXL3_K(2) EXL3_K(3) EXL3_K(4) EXL3_K(5) EXL3_K(6) EXL3_K(7) EXL3_K(8)
 #undef EXL3_K

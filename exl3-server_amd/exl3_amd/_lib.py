@@ -56,9 +56,14 @@ class MoeLayerDesc(C.Structure):
                 ("router_w", C.c_void_p), ("router_bias", C.c_void_p)]
 
 
+# exl3_weight_form
+FORM_REFERENCE = 0
+FORM_HALVES = 1
+
+
 class Tuning(C.Structure):
     _fields_ = [("rows_per_pass", C.c_int32), ("mat_min_rows", C.c_int32),
-                ("mat_max_rows", C.c_int32)]
+                ("mat_max_rows", C.c_int32), ("weight_form", C.c_int32)]
 
 
 class PathInfo(C.Structure):

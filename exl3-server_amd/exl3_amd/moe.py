@@ -187,9 +187,11 @@ class DeviceMoeLayer:
         call("exl3_moe_timing_get", self.handle, C.byref(t))
         return {k: getattr(t, k) for k, _ in MoeTiming._fields_}
 
-    def set_tuning(self, rows_per_pass=0, mat_min_rows=16, mat_max_rows=0):
-        """This handle's tuning knobs (exl3_moe_set_tuning); no knob moves an output bit."""
-        call("exl3_moe_set_tuning", self.handle, C.byref(Tuning(rows_per_pass, mat_min_rows, mat_max_rows)))
+    def set_tuning(self, rows_per_pass=0, mat_min_rows=16, mat_max_rows=0, weight_form=0):
+        """This handle's tuning knobs (exl3_moe_set_tuning). Only weight_form moves output
+        bits: 0 = the reference's f16 weights (default), 1 = exact halves (mcg/3inst)."""
+        call("exl3_moe_set_tuning", self.handle,
+             C.byref(Tuning(rows_per_pass, mat_min_rows, mat_max_rows, weight_form)))
 
     def tuning(self) -> dict:
         t = Tuning()

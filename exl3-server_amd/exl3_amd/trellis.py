@@ -178,15 +178,16 @@ def trellis_linear_group_rows_scaled(ws_list, x, rows, suh_stack, svh_stack):
     return _grouped(ws_list, x, rows, False, suh_stack, svh_stack)
 
 
-def trellis_set_tuning(rows_per_pass=0, mat_min_rows=16, mat_max_rows=0) -> None:
-    call("exl3_set_tuning", C.byref(Tuning(rows_per_pass, mat_min_rows, mat_max_rows)))
+def trellis_set_tuning(rows_per_pass=0, mat_min_rows=16, mat_max_rows=0, weight_form=0) -> None:
+    """Process-wide knobs of the single/grouped linear (exl3_set_tuning). weight_form:
+    0 = the reference's f16 weights (default), 1 = exact halves (mcg/3inst only)."""
+    call("exl3_set_tuning", C.byref(Tuning(rows_per_pass, mat_min_rows, mat_max_rows, weight_form)))
 
 
 def trellis_get_tuning() -> dict:
     t = Tuning()
     call("exl3_get_tuning", C.byref(t))
-    return dict(rows_per_pass=t.rows_per_pass, mat_min_rows=t.mat_min_rows,
-                mat_max_rows=t.mat_max_rows)
+    return {k: getattr(t, k) for k, _ in Tuning._fields_}
 
 
 def trellis_path_info(w: TrellisWeight, rows: int) -> dict:

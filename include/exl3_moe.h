@@ -89,16 +89,34 @@ typedef struct {
   const float *router_bias;         /* device f32 (E) */
 } exl3_moe_layer_desc;
 
+/* The weights an mcg/3inst GEMV multiplies (exl3_tuning.weight_form). A weight of these
+ * codebooks is the sum of the two f16 halves of its masked hash word (exl3.cpp:36-42).
+ * mul1 has one form (one f16 fma per weight, trellis_gemm.cpp:336-345). */
+typedef enum {
+  /* Default. Each weight rounded to f16 once, half(lo + hi), exactly the value the
+   * reference's QMV multiplies (trellis_gemm.cpp:348-356) and the bits of
+   * exl3_trellis_decode. */
+  EXL3_FORM_REFERENCE = 0,
+  /* Opt-in. x*lo + x*hi summed in f32, without the f16 rounding of lo + hi: one VALU
+   * instruction per weight less and twice the MFMAs. Outputs differ from the reference's
+   * by the weights' f16 rounding (at most 2^-11 of each weight); a SwiGLU clamp that
+   * cuts large gate/up outputs can amplify that to percents of the output RMS. */
+  EXL3_FORM_HALVES = 1
+} exl3_weight_form;
+
 /* Scheduling knobs. Mirrors TrellisTuning (trellis_gemm.h:137-145): rows_per_pass is
  * the linear's token rows per MFMA pass (the reference's mb; 1..16), mat_min_rows and
  * mat_max_rows the reference's staged-path window (0 = off / no cap), reported by
  * exl3_trellis_path_info. Every pass runs on the matrix cores here, so the staged
- * window only labels calls. None of them changes an output bit (the k-split partition
- * is a function of the tensor shape only). */
+ * window only labels calls. None of these three changes an output bit (the k-split
+ * partition is a function of the tensor shape only). weight_form (no counterpart in
+ * the reference, whose Metal QMV has the reference form only) selects the mcg/3inst
+ * weights: EXL3_FORM_REFERENCE (0, the default) or EXL3_FORM_HALVES. */
 typedef struct {
   int32_t rows_per_pass;  /* 0 = auto: min(rows, 16), one MFMA pass */
   int32_t mat_min_rows;   /* calls of >= this many rows count as staged (default 16) */
   int32_t mat_max_rows;   /* 0 = no cap */
+  int32_t weight_form;    /* exl3_weight_form */
 } exl3_tuning;
 
 /* What a trellis linear at `rows` rows will do. Mirrors TrellisPathInfo
@@ -281,7 +299,10 @@ exl3_status exl3_moe_timing_reset(exl3_moe_layer_t layer);
 /* The handle's own copy of the tuning knobs (TrellisTuning, trellis_gemm.h:137-145,
  * which the reference keeps process-global). It starts as exl3_get_tuning() at
  * exl3_moe_layer_create; its mat_min_rows/mat_max_rows window decides which runs the
- * diagnostics count as staged. No knob changes an output bit. */
+ * diagnostics count as staged, and its weight_form the weights of the mcg/3inst expert
+ * GEMVs (the only knob that changes output bits). Rejected (EXL3_ERR_INVALID) for a
+ * weight_form outside exl3_weight_form. Not to be changed while a call on the handle
+ * is being enqueued. */
 exl3_status exl3_moe_set_tuning(exl3_moe_layer_t layer, const exl3_tuning *t);
 exl3_status exl3_moe_get_tuning(exl3_moe_layer_t layer, exl3_tuning *t);
 

@@ -10,6 +10,9 @@ int main(void) {
   exl3_tuning t;
   if (exl3_get_tuning(&t) != EXL3_OK) return 2;
   if (exl3_set_tuning(&t) != EXL3_OK) return 3;
+  if (t.weight_form != EXL3_FORM_REFERENCE) return 6;
+  t.weight_form = 7;
+  if (exl3_set_tuning(&t) != EXL3_ERR_INVALID) return 7;
   exl3_trellis_desc d;
   memset(&d, 0, sizeof d);
   d.trellis = (const void *)0x1000;

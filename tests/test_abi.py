@@ -22,14 +22,22 @@ def test_library_exports_every_header_symbol():
 
 def test_abi_version_and_tuning_roundtrip():
     L = _lib.lib()
-    assert L.exl3_abi_version() == 1
+    assert L.exl3_abi_version() == 2
     t0 = _lib.Tuning()
     _lib.call("exl3_get_tuning", C.byref(t0))
-    assert t0.mat_min_rows == 16
-    _lib.call("exl3_set_tuning", C.byref(_lib.Tuning(2, 0, 0)))
+    # the reference's f16 weights by default
+    assert t0.mat_min_rows == 16 and t0.weight_form == _lib.FORM_REFERENCE
+    _lib.call("exl3_set_tuning", C.byref(_lib.Tuning(2, 0, 0, _lib.FORM_HALVES)))
     t1 = _lib.Tuning()
     _lib.call("exl3_get_tuning", C.byref(t1))
-    assert (t1.rows_per_pass, t1.mat_min_rows) == (2, 0)
+    assert (t1.rows_per_pass, t1.mat_min_rows, t1.weight_form) == (2, 0, _lib.FORM_HALVES)
+    # a weight form outside the enum is refused and leaves the knobs as they were
+    for bad in (2, -1):
+        assert L.exl3_set_tuning(C.byref(_lib.Tuning(0, 16, 0, bad))) == 1
+        assert b"weight_form" in L.exl3_last_error()
+    t2 = _lib.Tuning()
+    _lib.call("exl3_get_tuning", C.byref(t2))
+    assert t2.weight_form == _lib.FORM_HALVES
     _lib.call("exl3_set_tuning", C.byref(t0))
 
 

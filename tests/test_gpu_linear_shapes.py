@@ -8,8 +8,9 @@ make_trellis, :60-76; mul1 as there, plus mcg and 3inst on three classes):
     oracle's f64 linear on the sub-tensor of those columns (a column block of a trellis
     tensor is itself a trellis tensor: its tiles (tk, tn) for tn in the block, with the
     block's svh), at the north-star bound (max |err| <= 2e-2 * rms, cosine >= 0.9999)
-    against the reference-rounded weights and within 2 output ulps of the exact-halves
-    oracle (the bound of test_linear_random_shapes). At most a quarter of the sampled
+    and within 2 output ulps (the bound of test_linear_random_shapes) of the oracle on
+    the reference's f16 weights; the mcg/3inst classes also in the opt-in exact-halves
+    weight form against the oracle's exact-halves mode. At most a quarter of the sampled
     outputs of a class may differ from the oracle at all: a yhat element within f32
     round-off of an f16 rounding boundary (about 0.5% of them) moves every output of its
     128-block by about 1/8 ulp through the output Hadamard, so about half the blocks carry
@@ -55,9 +56,10 @@ REAL_SHAPES = [
     ("mla_kv_a_k6", 4096, 512, 6, 2),
     ("mla_kv_a_k5", 4096, 512, 5, 2),
     ("mla_kv_a_k4", 4096, 512, 4, 2),
-    # the halves codebooks on three classes
+    # mcg and 3inst on four classes
     ("kda_qkv_proj_mcg", 4096, 24576, 4, 1),
     ("mla_o_proj_k6_3inst", 16384, 4096, 6, 0),
+    ("exp_gate_up_k4_3inst", 4096, 2048, 4, 0),
     ("lm_head_mcg", 4096, 154880, 6, 1),
 ]
 ROWS = (1, 2, 3, 4, 13, 26)
@@ -86,6 +88,21 @@ def test_real_shape_class(oracle, dev, name, in_f, out_f, K, cb):
     tiles = words.view(in_f // 16, out_f // 16, 16 * K)
     subs = {b: tiles[:, 8 * b:8 * b + 8, :].contiguous().cpu().numpy().view(np.uint16) for b in blocks}
     differ, checked = 0, 0
+    for form in ((0, 1) if cb != 2 else (0,)):
+        trellis_set_tuning(weight_form=form)
+        try:
+            d, c = _class_rows(oracle, dev, w, subs, blocks, name, in_f, K, cb, su, sv, form)
+        finally:
+            trellis_set_tuning()
+        differ += d
+        checked += c
+    assert differ <= 0.25 * checked, (differ, checked)
+    del w, words
+    torch.cuda.empty_cache()
+
+
+def _class_rows(oracle, dev, w, subs, blocks, name, in_f, K, cb, su, sv, form):
+    differ, checked = 0, 0
     for rows in ROWS:
         xb = synth.activations(SEED, f"cls.{name}.x{rows}", rows, in_f)
         x = torch.from_numpy(xb.view(np.float16)).to(dev)
@@ -95,28 +112,23 @@ def test_real_shape_class(oracle, dev, name, in_f, out_f, K, cb):
         for r in sorted({0, rows // 2, rows - 1}):
             assert np.array_equal(bits(trellis_linear(w, x[r:r + 1].contiguous())), got[r:r + 1]), (rows, r)
         if rows in (4, 26):
-            try:
-                for mb in (1, 3, 16):
-                    trellis_set_tuning(rows_per_pass=mb)
-                    assert np.array_equal(bits(trellis_linear(w, x)), got), (rows, mb)
-            finally:
-                trellis_set_tuning()
+            for mb in (1, 3, 16):
+                trellis_set_tuning(rows_per_pass=mb, weight_form=form)
+                assert np.array_equal(bits(trellis_linear(w, x)), got), (rows, mb)
+            trellis_set_tuning(weight_form=form)
         if rows not in ORACLE_ROWS:
             continue
         for b in blocks:
             cols = slice(128 * b, 128 * b + 128)
             g = got[:, cols].view(np.float16).astype(np.float64)
-            want = oracle.trellis_linear(subs[b], in_f, 128, K, cb, su, sv[cols], xb)
-            north_star(g, want.view(np.float16).astype(np.float64).reshape(g.shape))
-            with oracle.gemv_mode(True):
-                exact = oracle.trellis_linear(subs[b], in_f, 128, K, cb, su, sv[cols], xb)
-            r = exact.view(np.float16).astype(np.float64).reshape(g.shape)
+            with oracle.gemv_mode(form == 1):
+                want = oracle.trellis_linear(subs[b], in_f, 128, K, cb, su, sv[cols], xb)
+            r = want.view(np.float16).astype(np.float64).reshape(g.shape)
+            north_star(g, r)
             # yhat is rounded to f16 before the output Hadamard: within 2 ulps of the
             # block's largest output
             ulp = 2.0 ** (np.floor(np.log2(np.abs(r).max())) - 10)
-            assert np.max(np.abs(g - r)) <= 2 * ulp, (rows, b, np.max(np.abs(g - r)), ulp)
-            differ += int(np.sum(got[:, cols].reshape(-1) != exact.reshape(-1)))
-            checked += exact.size
-    assert differ <= 0.25 * checked, (differ, checked)
-    del w, words
-    torch.cuda.empty_cache()
+            assert np.max(np.abs(g - r)) <= 2 * ulp, (rows, b, form, np.max(np.abs(g - r)), ulp)
+            differ += int(np.sum(got[:, cols].reshape(-1) != want.reshape(-1)))
+            checked += want.size
+    return differ, checked

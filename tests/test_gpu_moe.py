@@ -4,8 +4,10 @@ Routing: top-k id sets equal to the oracle's f64 routing, except where the k-th 
 (k+1)-th biased scores are closer than NEAR_TIE (reported, then the GPU's routing is
 used to check the experts' arithmetic). Layer output: the north-star tolerance,
 max |err| <= 2e-2 * rms(reference) and cosine >= 0.9999, against the oracle on the
-reference's f16 weights; the random stress layers also against the oracle's
-exact-halves mode (check_out_both).
+reference's f16 weights (the default weight form). The opt-in exact-halves form
+(exl3_tuning.weight_form = 1) is held to the same bound against the oracle's
+exact-halves mode (check_out_forms); the limit-0.5 cases are layers where the two
+forms differ by more than that bound, so each form must match its own oracle.
 Invariants of the reference (moe_test.cpp (g)/(h)): an N-row call equals N single-row
 calls bit for bit; the run grouping equals the oracle's.
 """
@@ -15,6 +17,7 @@ import torch
 
 from exl3_amd import synth
 from exl3_amd.moe import DeviceMoeLayer, moe_topk_route, trellis_words_torch
+from layer_cases import LIMIT_HALF_CASES, limit_half_case, random_cfgs
 
 pytestmark = pytest.mark.gpu
 
@@ -62,22 +65,20 @@ def _masked_choice_scores(sfc, n_group, topk_group):
     return np.where(np.repeat(keep, E // ng), sfc, -np.inf), gap
 
 
-def check_out_both(oracle, got_t, routed_args):
-    """The layer against both oracle modes. Exact halves (the weights the GEMV multiplies,
-    see test_gpu_trellis): the north-star bound. Reference-rounded weights: the
-    north-star bound, or twice the oracle's own deviation between its two modes where
-    that is larger. That deviation measures how far the reference's own f16 rounding of
-    yhat (before the output Hadamard) lets a one-ulp change of any weight move this
-    input's output: it is small at GLM-5's SwiGLU limit (<= 0.6% of the RMS) and reaches
-    3% where a limit of 0.5 clips gate/up outputs of RMS 30."""
-    want = oracle.moe_layer_routed(*routed_args)
+def check_out_forms(oracle, d, x, got_t, routed_args):
+    """The layer in both weight forms against the matching oracle mode, each at the
+    got_t (the default form: the reference's f16 weights) against the
+    reference-rounded oracle, then the handle's exact-halves form against the oracle's
+    exact-halves mode. Returns the default form's (err/rms, cosine)."""
+    res = check_out(got_t, oracle.moe_layer_routed(*routed_args))
+    d.set_tuning(weight_form=1)
+    try:
+        y_h = d(x)
+    finally:
+        d.set_tuning()
     with oracle.gemv_mode(True):
-        exact = oracle.moe_layer_routed(*routed_args)
-    check_out(got_t, exact)
-    a = want.view(np.float16).astype(np.float64)
-    b = exact.view(np.float16).astype(np.float64)
-    dev = np.max(np.abs(a - b)) / np.sqrt(np.mean(a ** 2))
-    return check_out(got_t, want, tol=max(TOL_RMS, 2 * dev))
+        check_out(y_h, oracle.moe_layer_routed(*routed_args))
+    return res
 
 
 def check_routing(oracle, logits, bias, ids_gpu, cfg):
@@ -656,31 +657,6 @@ def test_layer_large_hidden_many_slices(oracle, dev):
     d.close()
 
 
-def random_cfgs(n, seed):
-    """n seeded layer configurations over the shape space the kernels take: hidden and
-    intermediate multiples of 128, E up to 64 with optional group-limited routing,
-    top-k up to 8, every K and codebook, no / trellis / f16 shared expert."""
-    rng = np.random.default_rng(seed)
-    out = []
-    for _ in range(n):
-        E = int(rng.choice([4, 8, 12, 16, 40, 64]))
-        groups = [g for g in (1, 2, 4) if E % g == 0 and E // g >= 2]
-        ng = int(rng.choice(groups))
-        tg = int(rng.integers(1, ng + 1))
-        topk = int(rng.integers(1, min(8, E * tg // ng) + 1))
-        shared = int(rng.integers(0, 3))  # 0 none, 1 trellis, 2 f16
-        out.append(synth.MoeConfig(
-            hidden=128 * int(rng.integers(1, 6)), inter=128 * int(rng.integers(1, 4)), n_experts=E,
-            top_k=topk, n_group=ng, topk_group=tg, norm_topk_prob=bool(rng.integers(0, 2)),
-            routed_scaling_factor=float(rng.choice([1.0, 1.5, 2.5])),
-            swiglu_limit=float(rng.choice([0.5, 7.0, 10.0])),
-            shared_inter=128 * int(rng.integers(1, 3)) if shared else 0,
-            gate_up_K=int(rng.integers(1, 9)), gate_up_cb=int(rng.integers(0, 3)),
-            down_K=int(rng.integers(1, 9)), down_cb=int(rng.integers(0, 3)),
-            shared_K=int(rng.integers(1, 9)) if shared == 1 else 0, shared_cb=int(rng.integers(0, 3))))
-    return out
-
-
 @pytest.mark.parametrize("i", range(24))
 def test_layer_random_shapes(oracle, dev, i):
     # seeded random configurations at a row count each that walks the dispatch and path
@@ -700,9 +676,26 @@ def test_layer_random_shapes(oracle, dev, i):
     idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
     args = (oc, [l.oracle_dict() for l in layer.experts],
             [l.oracle_dict() for l in layer.shared] if has_shared else None, h, idx, w)
-    check_out_both(oracle, y, args)
+    check_out_forms(oracle, d, x, y, args)
     r = B // 2
     assert torch.equal(d(x[r:r + 1].contiguous()).view(-1).cpu(), y.view(B, -1).cpu()[r]), (cfg, B)
+    d.close()
+
+
+@pytest.mark.parametrize("seed,i,B", LIMIT_HALF_CASES)
+def test_layer_limit_half_each_form_its_oracle(oracle, dev, seed, i, B):
+    cfg, layer, h = limit_half_case(seed, i, B)
+    d = DeviceMoeLayer(layer, dev)
+    x = to_dev(h, dev, B, 1, cfg.hidden)
+    y = d(x)
+    _, ids = d.route(x)
+    has_shared = cfg.shared_inter > 0
+    oc = ocfg_of(oracle, cfg, has_shared)
+    idx, w, _ = check_routing(oracle, oracle.router_logits(h, layer.router_w), layer.bias,
+                              ids.cpu().numpy(), oc)
+    args = (oc, [l.oracle_dict() for l in layer.experts],
+            [l.oracle_dict() for l in layer.shared] if has_shared else None, h, idx, w)
+    check_out_forms(oracle, d, x, y, args)
     d.close()
 
 

@@ -1,15 +1,17 @@
 """GPU parity tests of the trellis tensor path through the C ABI.
 
 Bit-exact against the oracle: decode (W_hat), reconstruct (W), the Hadamard steps.
-Tolerance (stated per test) against the oracle's f64 GEMV: matmul_raw and linear. For
-mcg/3inst the GEMV feeds both f16 halves of a weight's masked hash word to the matrix
-cores, i.e. multiplies the exact sum lo + hi where the reference multiplies its f16
-rounding: the tight bounds are taken against the oracle's exact-halves mode
-(oracle.gemv_mode(True)), and the reference-rounded oracle is met at the north-star
-tolerance (max |err| <= 2e-2 * rms, cosine >= 0.9999).
+Tolerance (stated per test) against the oracle's f64 GEMV: matmul_raw and linear. The
+default weight form multiplies the reference's f16 weights (trellis_gemm.cpp:348-356),
+the same values the oracle's default mode multiplies, so the tight f32-accumulation
+bounds hold against it. The opt-in exact-halves form (exl3_tuning.weight_form = 1,
+mcg/3inst) multiplies lo + hi unrounded and is held to the same tight bounds against
+the oracle's exact-halves mode (oracle.gemv_mode(True)).
 Bit-exact invariants of the reference (tests/glm5_gemv_nt_test.cpp, moe_test.cpp):
 the row-block knob moves no byte, grouped == per-member, rows == single rows.
 """
+import contextlib
+
 import numpy as np
 import pytest
 import torch
@@ -22,6 +24,17 @@ from exl3_amd.trellis import (TrellisWeight, f16_from_bits, trellis_decode, trel
 
 pytestmark = pytest.mark.gpu
 SEED = 77
+
+
+@contextlib.contextmanager
+def weight_form(oracle, form):
+    """The process-wide weight form of the linear and the matching oracle mode."""
+    trellis_set_tuning(weight_form=form)
+    try:
+        with oracle.gemv_mode(form == 1):
+            yield
+    finally:
+        trellis_set_tuning()
 
 
 def make(dev, in_f, out_f, K, cb, name, scale_std=0.05):
@@ -99,23 +112,29 @@ def north_star(got_bits, want_bits):
     assert np.max(np.abs(g - r)) <= 2e-2 * rms and cos >= 0.9999, (np.max(np.abs(g - r)), rms, cos)
 
 
-@pytest.mark.parametrize("K,cb", [(1, 2), (2, 0), (3, 1), (4, 1), (5, 1), (6, 0), (8, 2)])
-def test_matmul_raw_vs_f64(oracle, dev, K, cb):
+MM_CASES = [(1, 2, 0), (2, 0, 0), (3, 1, 0), (4, 1, 0), (5, 1, 0), (6, 0, 0), (8, 2, 0),
+            (2, 0, 1), (4, 1, 1), (5, 1, 1), (7, 0, 1)]
+
+
+@pytest.mark.parametrize("K,cb,form", MM_CASES)
+def test_matmul_raw_vs_f64(oracle, dev, K, cb, form):
     in_f, out_f, rows = 4096, 1024, 3
     w, words, _, _ = make(dev, in_f, out_f, K, cb, f"mm.{K}.{cb}")
     xh = synth.normal_f16(SEED, f"mm.x.{K}", (rows, in_f), 0.0, 1.0)
-    got = trellis_matmul_raw(w, torch.from_numpy(xh.view(np.float16)).to(dev)).cpu().numpy()
     what = oracle.decode_inner(words, in_f, out_f, K, cb)
     bound = gemv_bound(xh, what)
-    with oracle.gemv_mode(True):
-        exact = oracle.matmul_raw(words, in_f, out_f, K, cb, xh)
-    assert np.all(np.abs(got - exact) <= bound)
-    # against the reference's f16 weights: the f32 bound plus each weight's f16 rounding
-    # (at most 2^-11 of it; none for mul1, whose weights the GEMV computes exactly)
-    want = oracle.matmul_raw(words, in_f, out_f, K, cb, xh)
-    wr = 0.0 if cb == 2 else 2.0 ** -11
-    x = np.abs(xh.view(np.float16).astype(np.float64))
-    assert np.all(np.abs(got - want) <= bound + wr * (x @ np.abs(what.view(np.float16).astype(np.float64))))
+    with weight_form(oracle, form):
+        got = trellis_matmul_raw(w, torch.from_numpy(xh.view(np.float16)).to(dev)).cpu().numpy()
+        want = oracle.matmul_raw(words, in_f, out_f, K, cb, xh)
+    assert np.all(np.abs(got - want) <= bound)
+    if form == 1:
+        # against the reference's f16 weights: the f32 bound plus each weight's f16
+        # rounding (at most 2^-11 of it)
+        ref = oracle.matmul_raw(words, in_f, out_f, K, cb, xh)
+        x = np.abs(xh.view(np.float16).astype(np.float64))
+        extra = 2.0 ** -11 * (x @ np.abs(what.view(np.float16).astype(np.float64)))
+        assert np.all(np.abs(got - ref) <= bound + extra)
+        assert not np.array_equal(got, ref.astype(np.float32))
 
 
 # f16 output tolerance of one linear: the f32-vs-f64 GEMV difference can move the f16
@@ -123,22 +142,40 @@ def test_matmul_raw_vs_f64(oracle, dev, K, cb):
 LIN_TOL_RMS = 2e-3
 
 
-@pytest.mark.parametrize("K", range(1, 9))
-@pytest.mark.parametrize("cb", [0, 1, 2])
-def test_linear_sweep_4096(oracle, dev, K, cb):
-    # in = out = 4096, rows = 1
-    w, words, su, sv = make(dev, 4096, 4096, K, cb, f"lin.{K}.{cb}")
-    x = synth.activations(SEED, f"lin.x.{K}.{cb}", 1, 4096)
-    got = bits(trellis_linear(w, torch.from_numpy(x.view(np.float16)).to(dev)))
-    north_star(got, oracle.trellis_linear(words, 4096, 4096, K, cb, su, sv, x))
-    with oracle.gemv_mode(True):
-        want = oracle.trellis_linear(words, 4096, 4096, K, cb, su, sv, x)
+def check_linear_tight(got, want):
     g = got.view(np.float16).astype(np.float64)
-    r = want.view(np.float16).astype(np.float64)
+    r = want.view(np.float16).astype(np.float64).reshape(g.shape)
     rms = np.sqrt(np.mean(r ** 2))
     assert np.isfinite(g).all() and rms > 0.1
     assert np.max(np.abs(g - r)) <= LIN_TOL_RMS * rms
-    assert np.mean(got == want) > 0.9
+    assert np.mean(got.reshape(-1) == want.reshape(-1)) > 0.9
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_linear_sweep_4096(oracle, dev, K, cb):
+    # in = out = 4096, rows = 1, the default form against the reference's
+    # f16 weights
+    w, words, su, sv = make(dev, 4096, 4096, K, cb, f"lin.{K}.{cb}")
+    x = synth.activations(SEED, f"lin.x.{K}.{cb}", 1, 4096)
+    got = bits(trellis_linear(w, torch.from_numpy(x.view(np.float16)).to(dev)))
+    want = oracle.trellis_linear(words, 4096, 4096, K, cb, su, sv, x)
+    north_star(got, want)
+    check_linear_tight(got, want)
+
+
+@pytest.mark.parametrize("K", [1, 4, 5, 8])
+@pytest.mark.parametrize("cb", [0, 1])
+def test_linear_sweep_4096_halves_form(oracle, dev, K, cb):
+    # the opt-in exact-halves form on configs[1] against the oracle's exact-halves mode
+    w, words, su, sv = make(dev, 4096, 4096, K, cb, f"lin.{K}.{cb}")
+    x = synth.activations(SEED, f"lin.x.{K}.{cb}", 1, 4096)
+    with weight_form(oracle, 1):
+        got = bits(trellis_linear(w, torch.from_numpy(x.view(np.float16)).to(dev)))
+        want = oracle.trellis_linear(words, 4096, 4096, K, cb, su, sv, x)
+    check_linear_tight(got, want)
+    # and it is a different form: some outputs differ from the default form's
+    assert not np.array_equal(got, bits(trellis_linear(w, torch.from_numpy(x.view(np.float16)).to(dev))))
 
 
 def test_rows_invariance_and_row_block_knob(dev):
@@ -200,10 +237,10 @@ def test_dword_aligned_base(dev, K, cb):
 @pytest.mark.parametrize("i", range(12))
 def test_linear_random_shapes(oracle, dev, i):
     # seeded random linears (in and out multiples of 128 up to 1280, every K and
-    # codebook, 1..70 rows): the oracle's f64 linear (exact-halves mode) within the f16
-    # bound below and the reference-rounded one at the north-star tolerance, one row
-    # equal to that row alone, and the grouped call (this member twice) equal to the
-    # single call
+    # codebook, 1..70 rows), in each weight form against the oracle's f64 linear in the
+    # same form within the f16 bound below (the default form also at the north-star
+    # tolerance), one row equal to that row alone, and the grouped call (this member
+    # twice) equal to the single call
     rng = np.random.default_rng(9000 + i)
     in_f, out_f = 128 * int(rng.integers(1, 11)), 128 * int(rng.integers(1, 11))
     K, cb = int(rng.integers(1, 9)), int(rng.integers(0, 3))
@@ -211,23 +248,26 @@ def test_linear_random_shapes(oracle, dev, i):
     w, words, su, sv = make(dev, in_f, out_f, K, cb, f"rnd.{i}")
     xb = synth.activations(SEED, f"rnd.x.{i}", rows, in_f)
     x = torch.from_numpy(xb.view(np.float16)).to(dev)
-    got = bits(trellis_linear(w, x))
-    north_star(got, oracle.trellis_linear(words, in_f, out_f, K, cb, su, sv, xb))
-    with oracle.gemv_mode(True):
-        want = oracle.trellis_linear(words, in_f, out_f, K, cb, su, sv, xb)
-    g = got.view(np.float16).astype(np.float64)
-    r = want.view(np.float16).astype(np.float64).reshape(g.shape)
-    rms = np.sqrt(np.mean(r ** 2))
-    assert np.isfinite(g).all() and rms > 0.01, (in_f, out_f, K, cb, rows)
-    # yhat is rounded to f16 before the output Hadamard (trellis_gemm.cpp:397-399): where
-    # the f32 GEMV lands within its error of an f16 rounding boundary that yhat moves by
-    # one ulp, and the outputs of its 128-block move by at most one ulp of their own.
-    # So: within 2 ulps of the largest output, and almost all outputs bit-identical.
-    ulp = 2.0 ** (np.floor(np.log2(np.abs(r).max())) - 10)
-    err = np.max(np.abs(g - r))
-    assert err <= 2 * ulp, (in_f, out_f, K, cb, rows, err, ulp)
-    assert np.mean(got.reshape(-1) != want.reshape(-1)) <= 0.1, (in_f, out_f, K, cb, rows)
-    j = rows // 2
-    assert np.array_equal(bits(trellis_linear(w, x[j:j + 1].contiguous())), got[j:j + 1])
-    grp = bits(trellis_linear_group([w, w], x))
-    assert np.array_equal(grp[0], got) and np.array_equal(grp[1], got)
+    for form in ((0, 1) if cb != 2 else (0,)):
+        with weight_form(oracle, form):
+            got = bits(trellis_linear(w, x))
+            want = oracle.trellis_linear(words, in_f, out_f, K, cb, su, sv, xb)
+            if form == 0:
+                north_star(got, want)
+            g = got.view(np.float16).astype(np.float64)
+            r = want.view(np.float16).astype(np.float64).reshape(g.shape)
+            rms = np.sqrt(np.mean(r ** 2))
+            assert np.isfinite(g).all() and rms > 0.01, (in_f, out_f, K, cb, rows)
+            # yhat is rounded to f16 before the output Hadamard (trellis_gemm.cpp:397-399):
+            # where the f32 GEMV lands within its error of an f16 rounding boundary that
+            # yhat moves by one ulp, and the outputs of its 128-block move by at most one
+            # ulp of their own. So: within 2 ulps of the largest output, and almost all
+            # outputs bit-identical.
+            ulp = 2.0 ** (np.floor(np.log2(np.abs(r).max())) - 10)
+            err = np.max(np.abs(g - r))
+            assert err <= 2 * ulp, (in_f, out_f, K, cb, rows, form, err, ulp)
+            assert np.mean(got.reshape(-1) != want.reshape(-1)) <= 0.1, (in_f, out_f, K, cb, rows, form)
+            j = rows // 2
+            assert np.array_equal(bits(trellis_linear(w, x[j:j + 1].contiguous())), got[j:j + 1])
+            grp = bits(trellis_linear_group([w, w], x))
+            assert np.array_equal(grp[0], got) and np.array_equal(grp[1], got)

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 from exl3_amd import synth
+from layer_cases import LIMIT_HALF_CASES, limit_half_case
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -486,3 +487,23 @@ def test_oracle_swiglu_clip_like_mlx(oracle):
         else:
             rms = np.sqrt(np.mean(want ** 2))
             assert rms > 1e-4 and np.max(np.abs(got - want)) <= 2e-2 * rms
+
+
+@pytest.mark.parametrize("seed,i,B", LIMIT_HALF_CASES)
+def test_limit_half_cases_separate_the_forms(oracle, seed, i, B):
+    # the GPU parity cases at a SwiGLU limit of 0.5 (tests/layer_cases.py): the oracle on
+    # the reference's f16 weights and the oracle on exact halves differ by more than the
+    # north-star bound (2e-2 of the RMS), so a GEMV that multiplied the exact halves could
+    # not pass the reference-weight check there, and the other way round
+    cfg, layer, h = limit_half_case(seed, i, B)
+    has = cfg.shared_inter > 0
+    oc = oracle.make_cfg(cfg.hidden, cfg.inter, cfg.n_experts, cfg.top_k, cfg.n_group, cfg.topk_group,
+                         cfg.norm_topk_prob, has, cfg.routed_scaling_factor, cfg.swiglu_limit)
+    ex = [l.oracle_dict() for l in layer.experts]
+    sh = [l.oracle_dict() for l in layer.shared] if has else None
+    ref, _, _ = oracle.moe_layer(oc, ex, sh, layer.router_w, layer.bias, h)
+    with oracle.gemv_mode(True):
+        exact, _, _ = oracle.moe_layer(oc, ex, sh, layer.router_w, layer.bias, h)
+    a = ref.view(np.float16).astype(np.float64)
+    b = exact.view(np.float16).astype(np.float64)
+    assert np.max(np.abs(a - b)) > 2e-2 * np.sqrt(np.mean(a ** 2))
