@@ -92,5 +92,7 @@ exl3_status launch_hc_prepare(const exl3_hc_site *hc, const uint16_t *streams, i
 // Hands device buffers made by the loader to a layer handle, which frees them at
 // exl3_moe_layer_destroy; `in_place`/`repacked` count its trellis tensors.
 void layer_adopt(exl3_moe_layer_t layer, const std::vector<void *> &bufs, int64_t in_place, int64_t repacked);
+// The layer's hidden size.
+int layer_hidden(exl3_moe_layer_t layer);
 
 }  // namespace exl3h

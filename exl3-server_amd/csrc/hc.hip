@@ -237,11 +237,13 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
     const float rs = row_sum(c);
     c = live ? c / rs + eps : 0.0f;
     // Sinkhorn: columns, then (iters - 1) x (rows, columns); the entries outside N x N
-    // are 0 and stay 0
-    c = c / (col_sum(c) + eps);
+    // are set to 0 at every step (a padded row or column sums to 0, so at eps = 0 its
+    // own division would be 0 / 0; the sums themselves run on every lane for the DPP)
+    auto norm = [&](float v, float sum) { return live ? v / (sum + eps) : 0.0f; };
+    c = norm(c, col_sum(c));
     for (int it = 0; it < iters - 1; ++it) {
-      c = c / (row_sum(c) + eps);
-      c = c / (col_sum(c) + eps);
+      c = norm(c, row_sum(c));
+      c = norm(c, col_sum(c));
     }
     if (live) comb_out[p * N * N + ci * N + cj] = c;
   }

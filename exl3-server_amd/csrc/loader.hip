@@ -22,6 +22,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <map>
@@ -615,6 +616,152 @@ exl3_status exl3_moe_layer_load(const char *const *shard_paths, int32_t n_shards
   layer_adopt(layer, L.owned, in_place_trellis, repacked_trellis);
   L.owned.clear();
   *out_layer = layer;
+  return EXL3_OK;
+}
+
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------
+// The MLP sub-block's own tensors (post_attention_layernorm, hc_ffn_*)
+// ---------------------------------------------------------------------------------
+namespace {
+
+// IEEE round to nearest, ties to even, double -> f16 bits (overflow to inf, NaN to the
+// quiet NaN 0x7e00): the conversion the reference's load_any applies to F32 and BF16
+// tensors (glm5.cpp:236-238, fp16.h:26-63).
+uint16_t f16_bits_rne(double x) {
+  if (std::isnan(x)) return 0x7e00;
+  const uint16_t sign = std::signbit(x) ? 0x8000 : 0x0000;
+  const double m = std::fabs(x);
+  if (m == 0.0) return sign;
+  if (std::isinf(m)) return sign | 0x7c00;
+  int e = 0;
+  const double fr = std::frexp(m, &e);  // m = fr * 2^e, fr in [0.5, 1)
+  if (e >= -13) {  // normal range: m >= 2^-14
+    double r = std::nearbyint(std::ldexp(fr, 11));  // 11 significant bits, [1024, 2048]
+    int ex = e + 14;
+    if (r >= 2048.0) {
+      r = 1024.0;
+      ex += 1;
+    }
+    if (ex > 30) return sign | 0x7c00;
+    return (uint16_t)(sign | (ex << 10) | ((uint32_t)r - 1024u));
+  }
+  const double r = std::nearbyint(std::ldexp(m, 24));  // subnormal: units of 2^-24
+  return (uint16_t)(sign | (r >= 1024.0 ? 0x0400u : (uint32_t)r));
+}
+
+double f16_bits_to_double(uint16_t h) {
+  const int s = h >> 15, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  double v = e == 0 ? std::ldexp((double)m, -24)
+                    : e == 31 ? (m ? NAN : INFINITY) : std::ldexp(1.0 + m / 1024.0, e - 15);
+  return s ? -v : v;
+}
+
+// bf16 -> f16 bits: widened to f32 (exact), then one RNE (fp16.h:70-75)
+uint16_t f16_from_bf16(uint16_t b) {
+  const uint32_t u = (uint32_t)b << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f16_bits_rne((double)f);
+}
+
+// One tensor as load_any reads it (glm5.cpp:205-281): `n` elements to f16 bits or to f32.
+exl3_status tensor_as(const Src &s, const std::string &name, int64_t n, std::vector<uint16_t> *h16,
+                      std::vector<float> *h32) {
+  int64_t numel = 1;
+  for (int i = 0; i < s.t.ndim; ++i) numel *= s.t.shape[i];
+  if (numel != n) return fail(EXL3_ERR_INVALID, name + ": expected " + std::to_string(n) + " elements");
+  const uint8_t *src = s.f->map + s.t.file_offset;
+  if (s.t.dtype != EXL3_ST_F16 && s.t.dtype != EXL3_ST_BF16 && s.t.dtype != EXL3_ST_F32)
+    return fail(EXL3_ERR_UNSUPPORTED, name + ": only F16, BF16 and F32 tensors are converted");
+  auto f16_at = [&](int64_t i) -> uint16_t {
+    uint16_t v16;
+    float v32;
+    switch (s.t.dtype) {
+      case EXL3_ST_F16: std::memcpy(&v16, src + 2 * i, 2); return v16;
+      case EXL3_ST_BF16: std::memcpy(&v16, src + 2 * i, 2); return f16_from_bf16(v16);
+      default: std::memcpy(&v32, src + 4 * i, 4); return f16_bits_rne((double)v32);
+    }
+  };
+  if (h16) {
+    h16->resize((size_t)n);
+    for (int64_t i = 0; i < n; ++i) (*h16)[(size_t)i] = f16_at(i);
+  } else {
+    h32->resize((size_t)n);
+    for (int64_t i = 0; i < n; ++i) {
+      if (s.t.dtype == EXL3_ST_F32) {
+        std::memcpy(&(*h32)[(size_t)i], src + 4 * i, 4);
+      } else {
+        // F16 widened; BF16 through its f16 value, as the reference does for f32 requests
+        (*h32)[(size_t)i] = (float)f16_bits_to_double(f16_at(i));
+      }
+    }
+  }
+  return EXL3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+exl3_status exl3_moe_layer_load_block(exl3_moe_layer_t layer, const char *const *shard_paths, int32_t n_shards,
+                                      const char *layer_prefix, exl3_hc_site *site, const uint16_t **norm_w,
+                                      exl3_stream_t stream) {
+  if (!layer || !shard_paths || n_shards <= 0 || !layer_prefix || !site || !norm_w)
+    return fail(EXL3_ERR_INVALID, "exl3_moe_layer_load_block: bad arguments");
+  const int N = site->mult, D = layer_hidden(layer);
+  if (N < 1 || N > 4) return fail(EXL3_ERR_UNSUPPORTED, "hc_mult must be 1..4 (the fused path's range)");
+  Loader L;
+  L.st = stream_of(stream);
+  struct Closer {
+    Loader &l;
+    ~Closer() {
+      for (auto *f : l.files) exl3_st_close(f);
+    }
+  } closer{L};
+  for (int i = 0; i < n_shards; ++i) {
+    exl3_st_file_t f = nullptr;
+    exl3_status rc = exl3_st_open(shard_paths[i], &f);
+    if (rc) return rc;
+    L.files.push_back(f);
+  }
+  const std::string lp(layer_prefix);
+  const int W = (2 + N) * N;
+  const char *keys[4] = {"post_attention_layernorm.weight", "hc_ffn_fn", "hc_ffn_base", "hc_ffn_scale"};
+  Src src[4];
+  for (int i = 0; i < 4; ++i) {
+    src[i] = L.find(lp + keys[i]);
+    if (!src[i].ok) return fail(EXL3_ERR_INVALID, "missing tensor " + lp + keys[i]);
+  }
+  if (src[1].t.ndim != 2 || src[1].t.shape[0] != W || src[1].t.shape[1] != (int64_t)N * D)
+    return fail(EXL3_ERR_INVALID, lp + "hc_ffn_fn must be ((2 + mult) * mult, mult * hidden)");
+  std::vector<uint16_t> nw;
+  std::vector<float> fn, base, scale;
+  exl3_status rc = tensor_as(src[0], lp + keys[0], D, &nw, nullptr);
+  if (!rc) rc = tensor_as(src[1], lp + keys[1], (int64_t)W * N * D, nullptr, &fn);
+  if (!rc) rc = tensor_as(src[2], lp + keys[2], W, nullptr, &base);
+  if (!rc) rc = tensor_as(src[3], lp + keys[3], 3, nullptr, &scale);
+  if (rc) return rc;
+  // one buffer: fn (16-byte aligned, as exl3_hc_prepare requires), base, scale, norm weight
+  const size_t o_fn = 0, o_base = align_up(fn.size() * 4, 256), o_scale = o_base + align_up(base.size() * 4, 256);
+  const size_t o_nw = o_scale + 256, total = o_nw + align_up(nw.size() * 2, 256);
+  void *buf = nullptr;
+  rc = L.dev_alloc(total, &buf);
+  if (rc) return rc;
+  uint8_t *b = (uint8_t *)buf;
+  EXL3_HIP(hipMemcpyAsync(b + o_fn, fn.data(), fn.size() * 4, hipMemcpyHostToDevice, L.st));
+  EXL3_HIP(hipMemcpyAsync(b + o_base, base.data(), base.size() * 4, hipMemcpyHostToDevice, L.st));
+  EXL3_HIP(hipMemcpyAsync(b + o_scale, scale.data(), scale.size() * 4, hipMemcpyHostToDevice, L.st));
+  EXL3_HIP(hipMemcpyAsync(b + o_nw, nw.data(), nw.size() * 2, hipMemcpyHostToDevice, L.st));
+  EXL3_HIP(hipStreamSynchronize(L.st));  // the host vectors leave scope
+  layer_adopt(layer, L.owned, 0, 0);
+  L.owned.clear();
+  site->fn = (const float *)(b + o_fn);
+  site->base = (const float *)(b + o_base);
+  site->scale = (const float *)(b + o_scale);
+  *norm_w = (const uint16_t *)(b + o_nw);
   return EXL3_OK;
 }
 

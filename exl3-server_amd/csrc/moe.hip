@@ -873,6 +873,7 @@ void layer_adopt(exl3_moe_layer_t layer, const std::vector<void *> &bufs, int64_
   layer->loaded_in_place += in_place;
   layer->loaded_repacked += repacked;
 }
+int layer_hidden(exl3_moe_layer_t layer) { return layer->H; }
 }  // namespace exl3h
 
 namespace {

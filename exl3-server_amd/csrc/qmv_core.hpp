@@ -232,9 +232,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBufNT = 2;           // non-temporal: the ring words are streamed once
 constexpr uint32_t kNoChunk = 0x80000000u;  // offset past any tensor: the load returns 0
-// Step offset past any tensor (tensors are below 1 GiB, buffer sizes are 31-bit): with
-// any lane offset (kNoChunk included) and up to 8 steps added, the sum stays above the
-// buffer size and below 2^32, so the load returns 0 and touches no memory.
+// Lane offset past any tensor (tensors are below 1 GiB, buffer sizes are 31-bit), added
+// to a lane's chunk offset (voffset, which the raw buffer's range check covers; the
+// scalar soffset is left at 0): with any chunk offset, kNoChunk included, the sum stays
+// at or above 1 GiB and below 2^32, so the load returns 0 and touches no memory.
 constexpr uint32_t kPastEnd = 0x40000000u;
 
 template <int K>
@@ -377,21 +378,24 @@ __device__ __forceinline__ void qmv_slice_items(SliceStream<K, PD> &S, int nstep
   const int wbase = (sl.kt * 2 + sl.nt) * 8 * K;
   const uint32_t *xa = xrow + sl.kt * kTw;
   const int smask = nsteps - 1, slg = __builtin_ctz(nsteps);
+  // lane offsets past the tensor for the loads after the last step
+  const uint32_t vd0 = S.vo0 + kPastEnd, vd1 = S.vo1 + kPastEnd;
   for (int it = 0; it < items; ++it) {
     f32x4 D0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, D1 = D0;
     for (int s0 = 0; s0 < nsteps; s0 += PD) {
       // the steps PD ahead: this item's, then the next item's first ones; past the last
-      // step the loads take an offset beyond the tensor, which returns zeros without a
+      // step the loads take lane offsets beyond the tensor, which return zeros without a
       // memory access (so every group issues the same instructions)
       const int tn = it * nsteps + s0 + PD;
-      const uint32_t next = tn < items * nsteps
-                                ? S.so0 + (uint32_t)(tn & smask) * S.step_bytes + (uint32_t)(tn >> slg) * kItemBytes
-                                : kPastEnd;
+      const bool past = tn >= items * nsteps;
+      const uint32_t next =
+          past ? 0u : S.so0 + (uint32_t)(tn & smask) * S.step_bytes + (uint32_t)(tn >> slg) * kItemBytes;
+      const uint32_t v0 = past ? vd0 : S.vo0, v1 = past ? vd1 : S.vo1;
 #pragma unroll
       for (int b = 0; b < PD; ++b) {
         uint32_t W[K + 1];
         step_words<K>(slot, wbase, sl.m, S.L[b], W);
-        step_load<K>(S.rsrc, S.vo0, S.vo1, next + b * S.step_bytes, S.L[b]);
+        step_load<K>(S.rsrc, v0, v1, past ? 0u : next + b * S.step_bytes, S.L[b]);
         mfma_step<K, CB>(W, xa + (s0 + b) * (kStepTiles * kTw), D0, D1);
       }
     }

@@ -133,6 +133,7 @@ SIGNATURES = {
     "exl3_st_data": (vp, [vp, C.c_char_p]),
     "exl3_moe_layer_load": (C.c_int, [P(C.c_char_p), i32, C.c_char_p, P(MoeConfig), P(vp), vp]),
     "exl3_moe_layer_load_info": (C.c_int, [vp, P(i64), P(i64)]),
+    "exl3_moe_layer_load_block": (C.c_int, [vp, P(C.c_char_p), i32, C.c_char_p, P(HcSite), P(vp), vp]),
     "exl3_moe_get_tuning": (C.c_int, [vp, P(Tuning)]),
     "exl3_hc_workspace_size": (sz, [i32, i32, i64]),
     "exl3_hc_prepare": (C.c_int, [P(HcSite), vp, i64, i32, vp, C.c_float, vp, vp, vp, vp, sz, vp]),

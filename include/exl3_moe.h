@@ -414,6 +414,20 @@ const void *exl3_st_data(exl3_st_file_t f, const char *name);  /* host pointer i
 exl3_status exl3_moe_layer_load(const char *const *shard_paths, int32_t n_shards, const char *prefix,
                                 const exl3_moe_config *cfg, exl3_moe_layer_t *out_layer,
                                 exl3_stream_t stream);
+/* The MLP sub-block's own tensors of one decoder layer, so that exl3_moe_block can run
+ * from shards. Replaces the loads of l.post_norm and l.hc_ffn_* in load_decoder_layer
+ * (glm5.cpp:409-415). layer_prefix is the decoder layer's key prefix ("model.layers.N.");
+ * the keys are post_attention_layernorm.weight (hidden), hc_ffn_fn ((2 + mult) * mult,
+ * mult * hidden), hc_ffn_base ((2 + mult) * mult) and hc_ffn_scale (3), converted as the
+ * reference's load_any (glm5.cpp:205-281): the norm weight to f16 (F16 as stored, BF16
+ * widened to f32 and rounded once to f16, F32 rounded to f16, both to nearest even), the
+ * hc tensors to f32 (F32 as stored, F16 widened, BF16 through that same f16 value). The
+ * caller sets site->mult, sinkhorn_iters and eps (the model's hc_mult, hc_sinkhorn_iters,
+ * hc_eps); the call fills site->fn/base/scale and *norm_w with device pointers into
+ * memory `layer` owns (freed by exl3_moe_layer_destroy). Synchronises `stream`. */
+exl3_status exl3_moe_layer_load_block(exl3_moe_layer_t layer, const char *const *shard_paths, int32_t n_shards,
+                                      const char *layer_prefix, exl3_hc_site *site, const uint16_t **norm_w,
+                                      exl3_stream_t stream);
 /* For a loaded layer: trellis tensors used in place and repacked (0, 0 otherwise). */
 exl3_status exl3_moe_layer_load_info(exl3_moe_layer_t layer, int64_t *in_place, int64_t *repacked);
 

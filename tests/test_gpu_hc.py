@@ -134,6 +134,23 @@ def test_hc_prepare_large_eps_and_iteration_count(oracle, dev, eps, iters):
     check_f16(out, coll, ulps=1, extra=collapse_cond(st))
 
 
+@pytest.mark.parametrize("N", [1, 2, 3])
+def test_hc_prepare_zero_eps_fewer_streams(oracle, dev, N):
+    # hc_mult below 4 leaves entries of the device's 4 x 4 Sinkhorn layout outside N x N;
+    # at hc_eps 0 their rows and columns sum to 0, and the reference (which has no such
+    # entries) stays finite: so must the device, and match the oracle
+    P, D = 3, 512
+    fn, base, scale = make_site(300 + N, N, D)
+    st = streams_of(301 + N, P, N, D)
+    site = DeviceHcSite.from_numpy(fn, base, scale, N, 20, 0.0, dev)
+    out, post, comb = hc_prepare(dev_f16(st, dev), site)
+    coll, opost, ocomb = oracle.hc_prepare(st, N, D, fn, base, scale, 20, 0.0)
+    assert np.isfinite(comb.cpu().numpy()).all() and np.isfinite(post.cpu().numpy()).all()
+    assert np.max(np.abs(post.cpu().numpy() - opost)) <= 2e-5
+    assert np.max(np.abs(comb.cpu().numpy() - ocomb)) <= 2e-5
+    check_f16(out, coll, ulps=1, extra=collapse_cond(st))
+
+
 def test_hc_mix_identity_roundtrip(dev):
     # the reference's expand -> mix identity: streams that are copies of x, post = 1 and
     # comb = I give out[n] = f16(bo + x) exactly (1 * bo and 1 * x are exact, the sum is

@@ -1,5 +1,5 @@
 """CPU tests of the safetensors shard reader (exl3_st_*, host-only C ABI) on the
-committed EXL3 fixtures (tests/golden/moe_shard_{a,b}.safetensors, written by
+committed EXL3 fixtures (tests/golden/moe_shard_{a,b,c}.safetensors, written by
 tests/golden/make_shard.py from the seeded generator): the header parse, the tensor table,
 every tensor's bytes against the generator, the alignment cases, and the reference's
 consistency checks on malformed files (safetensors.cpp:52-102)."""
@@ -33,7 +33,7 @@ def test_fixture_is_what_the_script_writes(tmp_path, monkeypatch):
     # regenerating the fixture gives the committed bytes
     monkeypatch.setattr(make_shard, "HERE", str(tmp_path))
     make_shard.main()
-    for x in "ab":
+    for x in "abc":
         with open(os.path.join(tmp_path, f"moe_shard_{x}.safetensors"), "rb") as f, \
                 open(os.path.join(GOLDEN, f"moe_shard_{x}.safetensors"), "rb") as g:
             assert f.read() == g.read()
@@ -55,6 +55,44 @@ def test_header_and_table(shards):
     # trellis tensors at every file alignment mod 4
     mods = {v["file_offset"] % 4 for tab in (ta, tb) for k, v in tab.items() if k.endswith(".trellis")}
     assert mods == {0, 1, 2, 3}
+
+
+def test_shard_c_table():
+    # layer 1: 3inst gate/up and shared expert without marker tensors, mcg down with its
+    # marker; the MLP sub-block tensors in the dtypes the block loader converts
+    from exl3_amd.loader import Shard
+    c = Shard(os.path.join(GOLDEN, "moe_shard_c.safetensors"))
+    try:
+        assert c.header_len % 4 == 3
+        t = c.tensors()
+        P, LP = make_shard.PREFIX_1, make_shard.LAYER_PREFIX_1
+        for e in range(make_shard.SHARD_CFG_1.n_experts):
+            for nm in ("gate_proj", "up_proj"):
+                assert P + f"experts.{e}.{nm}.trellis" in t
+                assert not any(P + f"experts.{e}.{nm}.{m}" in t for m in ("mcg", "mul1"))
+            assert P + f"experts.{e}.down_proj.mcg" in t
+        assert t[P + "shared_experts.down_proj.trellis"]["shape"] == (128 // 16, 256 // 16, 48)
+        assert not any(k.startswith(P + "shared_experts") and k.endswith((".mcg", ".mul1")) for k in t)
+        assert (t[LP + "post_attention_layernorm.weight"]["dtype"], t[LP + "hc_ffn_fn"]["dtype"],
+                t[LP + "hc_ffn_base"]["dtype"], t[LP + "hc_ffn_scale"]["dtype"]) == ("BF16", "F32", "BF16", "F16")
+        assert t[LP + "hc_ffn_fn"]["shape"] == (24, 4 * 256)
+        nw, fn, base, scale = make_shard.block1()
+        assert np.array_equal(c.data(LP + "post_attention_layernorm.weight"), nw)
+        assert np.array_equal(c.data(LP + "hc_ffn_fn"), fn)
+    finally:
+        c.close()
+
+
+def test_bf16_helper_rounds_to_nearest_even():
+    # the fixture's f32 -> bf16 rounding against an exact f64 restatement on edge cases
+    x = np.array([1.0, 1.00390625, 1.005859375, 1.0078125 * (1 + 2 ** -9), -3.14159, 65504.0,
+                  1e-5, 2.0 ** -130], np.float32)
+    b = make_shard.bf16_bits(x)
+    back = (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    for xi, bi in zip(x.astype(np.float64), back):
+        e = np.floor(np.log2(abs(xi)))
+        ulp = 2.0 ** (max(e, -126) - 7)
+        assert abs(bi - xi) <= ulp / 2
 
 
 def test_bytes_equal_the_generator(shards):

@@ -92,6 +92,52 @@ def test_rms_factor_and_fn_orientation(oracle, eps):
     assert np.array_equal(c2.view(np.float16), c1.view(np.float16) * np.float16(2))
 
 
+def test_scale_index_closed_form(oracle):
+    # fn one-hot (projection j reads element idx[j] of the flattened streams), a random
+    # base and three distinct scale entries: scale[0] acts on the pre logits, scale[1] on
+    # post, scale[2] on comb (glm5_hc.cpp:313-315). The closed form below builds each
+    # output from the one element its projection reads; a swapped scale index moves post,
+    # comb or the collapsed stream far outside the bounds (checked: every swap fails).
+    P, N, D = 3, 3, 40
+    streams, fn, base, _ = make(8, P, N, D)
+    W = (2 + N) * N
+    rng = np.random.default_rng(9)
+    idx = rng.choice(N * D, size=W, replace=False)
+    fn[:] = 0
+    fn[np.arange(W), idx] = 1
+    base[:] = rng.normal(size=W).astype(np.float32)
+    scale = np.array([1.7, 0.45, 2.6], np.float32)
+    coll, post, comb = oracle.hc_prepare(streams, N, D, fn, base, scale, 4, EPS)
+    s = streams.reshape(P, N * D).view(np.float16).astype(np.float64)
+    rms = 1 / np.sqrt((s ** 2).mean(1) + EPS)
+    b = base.astype(np.float64)
+    sig = lambda v: 1 / (1 + np.exp(-v))  # noqa: E731
+
+    def closed(sc):
+        w = s[:, idx] * rms[:, None]                       # (P, W)
+        pre = sig(w[:, :N] * sc[0] + b[:N]) + EPS
+        pst = 2 * sig(w[:, N:2 * N] * sc[1] + b[N:2 * N])
+        z = (w[:, 2 * N:] * sc[2] + b[2 * N:]).reshape(P, N, N)
+        c = np.exp(z - z.max(2, keepdims=True))
+        c = c / c.sum(2, keepdims=True) + EPS
+        c = c / (c.sum(1, keepdims=True) + EPS)
+        for _ in range(3):
+            c = c / (c.sum(2, keepdims=True) + EPS)
+            c = c / (c.sum(1, keepdims=True) + EPS)
+        col = (pre[:, :, None] * s.reshape(P, N, D)).sum(1)
+        return col, pst, c
+
+    sc = scale.astype(np.float64)
+    col, pst, c = closed(sc)
+    g = coll.view(np.float16).astype(np.float64).reshape(P, D)
+    assert np.all(np.abs(g - col) <= np.abs(np.spacing(col.astype(np.float16))).astype(np.float64))
+    assert np.allclose(post, pst, rtol=1e-12) and np.allclose(comb, c, rtol=1e-10)
+    for perm in ([1, 0, 2], [2, 1, 0], [0, 2, 1], [1, 2, 0], [2, 0, 1]):
+        col2, pst2, c2 = closed(sc[perm])
+        assert (np.max(np.abs(g - col2)) > 0.01 or np.max(np.abs(post - pst2)) > 0.01
+                or np.max(np.abs(comb - c2)) > 0.01), perm
+
+
 @pytest.mark.parametrize("eps", [EPS, 1e-3, 0.05])
 def test_n1_closed_form(oracle, eps):
     P, D = 3, 32
