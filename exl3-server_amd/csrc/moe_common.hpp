@@ -52,7 +52,7 @@ enum SharedKind { kSharedNone = 0, kSharedTrellis = 1, kSharedDense = 2 };
 // Everything a kernel of one layer call needs, passed by value.
 // Long-run mode (calls of more than 16 token rows): the expert kernels take passes of
 // up to kLongBlocks 16-row MFMA blocks per decode.
-constexpr int kLongBlocks = 3;
+constexpr int kLongBlocks = 4;
 constexpr int kLongRows = 16 * kLongBlocks;
 
 struct MoeArgs {

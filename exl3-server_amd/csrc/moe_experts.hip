@@ -18,14 +18,17 @@
 //                 4 waves, over act -> raw f32 slice partials in yhat_dn (the output
 //                 Hadamard and the routing weight are applied by k_moe_combine). Extra
 //                 leading workgroups compute the f16 shared expert's down partials.
-//  *_long         calls of many rows: 48-row passes, every k slice in one workgroup,
-//                 slice partials folded in registers; k_moe_rotate stages the rotated
-//                 gate/up inputs once per (slot, projection).
+//  *_long         calls of many rows: 64-row passes, every k slice in one workgroup,
+//                 one accumulator chain per output over the whole k range;
+//                 k_moe_rotate stages the rotated gate/up inputs once per (slot,
+//                 projection).
 //
-// Per token row and expert the arithmetic is exl3_trellis_linear's (same input
-// Hadamard, k slices and slice order, output Hadamard), and the MFMA rows of a pass
-// never mix, so a run of r rows gives the same bytes as r single-row calls, and a layer
-// call the same bytes as its experts evaluated one linear at a time.
+// In the short-run kernels the arithmetic per token row and expert is
+// exl3_trellis_linear's (same input Hadamard, k slices and slice order, output
+// Hadamard), and the MFMA rows of a pass never mix, so a run of r rows gives the same
+// bytes as r single-row calls, and a layer call the same bytes as its experts evaluated
+// one linear at a time. The long-run kernels (the counterpart of the reference's staged
+// path) accumulate over k in another association: within f32 round-off of it.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -248,19 +251,19 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kDnW
   }
 }
 
-// Long runs (calls of more than 16 token rows): 8-wave workgroups, wave w owns n-pair
+// Long runs (calls of 65 token rows or more): 8-wave workgroups, wave w owns n-pair
 // 8*cb + w, passes of up to kLongRows rows with kLongBlocks 16-row MFMA blocks per
-// decode (qmv_slice_rb), and every k slice of the tensor in one workgroup: the slice
-// partials are added in slice order in registers (acc = p0; acc += p1; ...), the
-// same f32 operations as the slice-order sum of the short-run path, so each output
-// bit matches it. One partial per output goes to slice position 0.
+// decode (qmv_slice_rb), and every k slice of the tensor in one workgroup: each
+// block's accumulators run on from the first k step to the last (the reference's staged
+// path likewise sums in its own association, within 1% of max |value| of its QMV by its
+// test, glm5_gemv_nt_test.cpp:221-247). One partial per output goes to slice position 0.
 using exl3m::kLongBlocks;
 using exl3m::kLongRows;
 constexpr int kLongThreads = 512;
-// Staging loads in flight per lane: gate/up stages a 4-step part of duplicated rows,
-// 48 rows x 32 chunks = 3 chunks per thread (one round); down a slice of plain rows,
-// 48 x 64 = 6 per thread (two rounds of 4, the last two clamped copies).
-constexpr int kStageBatchGu = 3;
+// Staging loads in flight per lane: a slice of 64 plain rows is 64 x 64 chunks, 8 per
+// thread (two rounds of 4); a 4-step part of duplicated rows (the halves form) 64 x 32,
+// 4 per thread (one round).
+constexpr int kStageBatchGu = 4;
 constexpr int kStageBatchDn = 4;
 
 // Work unit u of the long-run kernels: pass u of the dispatch's pass table, or (shared
@@ -278,16 +281,6 @@ __device__ __forceinline__ bool pass_info(const MoeArgs &a, int u, int shared_mo
   ri.off = a.pass_off[u];
   ri.len = a.pass_len[u];
   return true;
-}
-
-template <int RB>
-__device__ __forceinline__ void fold_partials(f32x4 (&acc)[RB][2], const f32x4 (&D)[RB][2], bool first) {
-#pragma unroll
-  for (int r = 0; r < RB; ++r)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[r][h][i] = first ? D[r][h][i] : acc[r][h][i] + D[r][h][i];
 }
 
 template <int K, int CB, int PD>
@@ -324,7 +317,7 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int q_lg = __builtin_ctz(q_row);
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
-    f32x4 acc[kLongBlocks][2], D[kLongBlocks][2];
+    f32x4 D[kLongBlocks][2];
     for (int sl = 0; sl < n_sl; ++sl) {
       for (int pt = 0; pt < n_parts; ++pt) {
         // the part of the pass's rows, already rotated by k_moe_rotate (x_rot rows of
@@ -348,10 +341,9 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
         __syncthreads();
         if (active)
           qmv_slice_rb<K, CB, PD, kLongBlocks>(base, k_tiles, out / 16, k0 / 16, np, part, xs, xs_stride,
-                                               nr, slot, D, pt == 0);
+                                               nr, slot, D, sl == 0 && pt == 0);
         __syncthreads();
       }
-      if (active) fold_partials<kLongBlocks>(acc, D, sl == 0);
     }
     if (active) {
       const int col = np * 32;
@@ -362,8 +354,8 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
           const int r = 16 * rb + d_row(i);
           if (r < nr) {
             float *y = a.yhat_gu + (int64_t)((ri.off + p0 + r) * 2 + proj) * n_sl * a.Imax + col;
-            y[d_col(0)] = acc[rb][0][i];
-            y[d_col(1)] = acc[rb][1][i];
+            y[d_col(0)] = D[rb][0][i];
+            y[d_col(1)] = D[rb][1][i];
           }
         }
     }
@@ -400,7 +392,7 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
 
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
-    f32x4 acc[kLongBlocks][2], D[kLongBlocks][2];
+    f32x4 D[kLongBlocks][2];
     for (int sl = 0; sl < n_sl; ++sl) {
       for (int pt = 0; pt < n_parts; ++pt) {
         const int k0 = (sl * n_parts + pt) * part_k;
@@ -422,10 +414,9 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
         __syncthreads();
         if (active)
           qmv_slice_rb<K, CB, PD, kLongBlocks>(tb.tr[2], k_tiles, a.H / 16, k0 / 16, np, part, xs, xs_stride,
-                                               nr, slot, D, pt == 0);
+                                               nr, slot, D, sl == 0 && pt == 0);
         __syncthreads();
       }
-      if (active) fold_partials<kLongBlocks>(acc, D, sl == 0);
     }
     if (active) {
       const int col = np * 32;
@@ -436,8 +427,8 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
           const int r = 16 * rb + d_row(i);
           if (r < nr) {
             float *y = a.yhat_dn + (int64_t)(ri.off + p0 + r) * a.S_dn * a.H + col;
-            y[d_col(0)] = acc[rb][0][i];
-            y[d_col(1)] = acc[rb][1][i];
+            y[d_col(0)] = D[rb][0][i];
+            y[d_col(1)] = D[rb][1][i];
           }
         }
     }

@@ -97,7 +97,7 @@ __host__ __device__ constexpr int staged_row_words(int k_tiles, bool dup) {
   return slice_words(k_tiles, dup) + 4;
 }
 // The long-run kernels stage a slice of duplicated rows in parts of at most 4 wave
-// steps (a part of 48 rows is ~50 KB of LDS, so that two 8-wave workgroups share a CU;
+// steps (a part of 64 rows is ~66 KB of LDS, so that two 8-wave workgroups share a CU;
 // a whole slice of plain rows is that size already).
 __host__ __device__ constexpr int long_part_steps(int k_tiles, bool dup) {
   return !dup || slice_steps(k_tiles) < 4 ? slice_steps(k_tiles) : 4;

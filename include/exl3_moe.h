@@ -308,7 +308,7 @@ exl3_status exl3_moe_get_tuning(exl3_moe_layer_t layer, exl3_tuning *t);
 
 /* MoeRowsDiag equivalents (glm5_moe.h:121-122). staged_runs counts runs whose row
  * count lies in the handle's staged window; streamed_bytes counts each run's expert
- * bytes once per weight pass (passes of min(rows, 16) rows, or of 48 rows in calls of
+ * bytes once per weight pass (passes of min(rows, 16) rows, or of 64 rows in calls of
  * 65 rows or more). */
 exl3_status exl3_moe_diag_enable(exl3_moe_layer_t layer, int32_t enabled);
 exl3_status exl3_moe_diag_get(exl3_moe_layer_t layer, exl3_moe_diag *out);
