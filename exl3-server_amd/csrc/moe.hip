@@ -29,7 +29,7 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
                               int shared_mode, bool dense, hipStream_t st);
 int moe_slices(int in);
 exl3_status launch_moe_act(const MoeArgs &a, int shared_mode, int dense_blocks, hipStream_t st);
-exl3_status launch_moe_rotate(const MoeArgs &a, bool shared_trellis, hipStream_t st);
+exl3_status launch_moe_rotate(const MoeArgs &a, int64_t slot0, int64_t n_slots, hipStream_t st);
 }
 
 namespace {
@@ -1649,21 +1649,14 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
     for (int i = 0; i < 5; ++i) EXL3_HIP(hipEventCreate(&layer->ev[i]));
     layer->ev_made = true;
   }
-  if (timed) EXL3_HIP(hipEventRecord(layer->ev[0], st));
-  rc = launch_logits_route(layer, a, a.weights, a.ids, 1, st);
-  if (rc) return rc;
-  if (timed) EXL3_HIP(hipEventRecord(layer->ev[1], st));
-
   const int H = layer->H;
-  // L3: routed gate/up (+ the f16 shared expert's gate/up partials)
   const bool dense_sh = layer->shared == exl3m::kSharedDense;
+  const bool trellis_sh = layer->shared == exl3m::kSharedTrellis;
   const int64_t units = a.fold ? m.max_passes : m.R;  // work units: runs or long-run passes
-  if (a.fold || a.xrot_rows) {
-    rc = launch_moe_rotate(a, layer->shared == exl3m::kSharedTrellis, st);
-    if (rc) return rc;
-  }
-  // long-run calls: a trellis shared expert (under one wave of the machine on its own)
-  // runs on the layer's second stream while the routed experts run on the caller's
+  // Long-run calls: a trellis shared expert (under one wave of the machine on its own)
+  // does not depend on the routing, so it runs on the layer's second stream from the
+  // start of the call: beside the router and the dispatch (latency-bound launches that
+  // leave most of the machine idle), then beside the routed experts.
   const bool side = a.fold && layer->side_made && side_stream_on();
   // Every return after the fork joins the side stream back into the caller's (an
   // unjoined fork would leave a graph capture of this call unable to end).
@@ -1680,6 +1673,7 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
     join_side(false);
     return r;
   };
+  if (timed) EXL3_HIP(hipEventRecord(layer->ev[0], st));
   if (side) {
     // one caller at a time records the fork and join (calls on other threads and
     // streams would otherwise interleave them)
@@ -1687,7 +1681,8 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
     EXL3_HIP(hipEventRecord(layer->fork, st));
     EXL3_HIP(hipStreamWaitEvent(layer->side, layer->fork, 0));
     forked = true;
-    rc = launch_shared_trellis(layer, a, N, layer->side);
+    rc = launch_moe_rotate(a, a.P, N, layer->side);  // the shared slots: row i at slot P + i
+    if (!rc) rc = launch_shared_trellis(layer, a, N, layer->side);
     if (rc) {
       join_side(true);
       return rc;
@@ -1697,6 +1692,19 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
       join_side(true);
       return hip_check(e, "hipEventRecord(join)");
     }
+  }
+  rc = launch_logits_route(layer, a, a.weights, a.ids, 1, st);
+  if (rc) return fail_joined(rc);
+  if (timed) {
+    const hipError_t e = hipEventRecord(layer->ev[1], st);
+    if (e != hipSuccess) return fail_joined(hip_check(e, "hipEventRecord"));
+  }
+  // L3: routed gate/up (+ the f16 shared expert's gate/up partials), after the input
+  // rotation of the routed slots (and of a trellis shared expert's slots when it runs on
+  // this stream)
+  if (a.fold || a.xrot_rows) {
+    rc = launch_moe_rotate(a, 0, (int64_t)a.P + (trellis_sh && !side ? N : 0), st);
+    if (rc) return fail_joined(rc);
   }
   rc = launch_moe_expert(0, layer->gu_K, kernel_cb(layer->gu_cb, a.weight_form), units, a, 0, dense_sh, st);
   if (rc) return fail_joined(rc);

@@ -439,18 +439,21 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
 // = had_pre(h[row], suh of the slot's expert and projection) in the staged k order, so
 // the gate/up workgroups of a pass (one per 256 output columns) copy it instead of each
 // rotating it again. One wave per (slot, projection), kRotBatch 128-blocks at a time;
-// slots [0, n_slots): routed slots, then (trellis shared expert) the N shared slots.
+// slots [slot0, slot0 + n_slots): routed slots (below P, from the dispatch) or the N
+// shared slots of a trellis shared expert (slot P + i is token row i, whatever the
+// routing: so they can be rotated before the dispatch has run).
 constexpr int kRotBatch = 8;
 
-__global__ __launch_bounds__(256) void k_moe_rotate(MoeArgs a, int n_slots) {
+__global__ __launch_bounds__(256) void k_moe_rotate(MoeArgs a, int slot0, int n_slots) {
   const int lane = threadIdx.x & 63;
   const int nblk = a.H / 128;
   const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (gw >= (int64_t)n_slots * 2) return;
   const int proj = (int)(gw & 1);
-  const int64_t slot = gw >> 1;
+  const int64_t slot = slot0 + (gw >> 1);
   const int e = slot < a.P ? a.slot_e[slot] : a.E;
-  const uint16_t *hrow = a.h + (int64_t)a.sorted_row[slot] * a.H + 2 * lane;
+  const int64_t row = slot < a.P ? a.sorted_row[slot] : slot - a.P;
+  const uint16_t *hrow = a.h + row * a.H + 2 * lane;
   const uint16_t *suh = a.suh_s[proj] + (int64_t)e * a.H + 2 * lane;
   uint32_t *out = reinterpret_cast<uint32_t *>(a.xrot + (slot * 2 + proj) * a.H);
   for (int b0 = 0; b0 < nblk; b0 += kRotBatch) {
@@ -759,13 +762,12 @@ exl3_status launch_moe_expert(int which, int K, int cb, int64_t runs, const MoeA
   return EXL3_OK;
 }
 
-// Long-run mode: x_rot of the P routed slots and, with a trellis shared expert, the N
-// shared slots.
-exl3_status launch_moe_rotate(const MoeArgs &a, bool shared_trellis, hipStream_t st) {
-  const int64_t n_slots = (int64_t)a.P + (shared_trellis ? a.N : 0);
+// x_rot of slots [slot0, slot0 + n_slots): the P routed slots (after the dispatch) and,
+// with a trellis shared expert, the N shared slots from P on (any time).
+exl3_status launch_moe_rotate(const MoeArgs &a, int64_t slot0, int64_t n_slots, hipStream_t st) {
   const int64_t waves = n_slots * 2;
   if (waves == 0) return EXL3_OK;
-  k_moe_rotate<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a, (int)n_slots);
+  k_moe_rotate<<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(a, (int)slot0, (int)n_slots);
   EXL3_LAUNCHED("k_moe_rotate");
   return EXL3_OK;
 }
