@@ -191,6 +191,16 @@ __global__ __launch_bounds__(256) void k_moe_pre_tiled(MoeArgs a) {
 // ---------------------------------------------------------------------------------
 constexpr int kMaxE = 1024;
 constexpr int kIdBatch = 16;  // pair experts per lane loaded at once by the counting sort
+// Chunks of the dispatch's counting sort, one workgroup each: 1024 pairs (a round of 64
+// per wave) up to kDispatchMaxWg chunks, above that kDispatchMaxWg chunks of a multiple of
+// 1024 pairs; one workgroup up to 1024 pairs.
+constexpr int kDispatchMaxWg = 64;
+__host__ __device__ constexpr int64_t dispatch_chunk_pairs(int64_t P) {
+  return 1024 * (((P + 1023) / 1024 + kDispatchMaxWg - 1) / kDispatchMaxWg);
+}
+__host__ __device__ constexpr int dispatch_wgs(int64_t P) {
+  return P > 0 ? (int)((P + dispatch_chunk_pairs(P) - 1) / dispatch_chunk_pairs(P)) : 1;
+}
 // Route kernels are instantiated for E <= 64 * JN experts (JN 64-expert chunks per lane).
 template <typename F>
 static void with_route_chunks(int E, F &&f) {
@@ -339,6 +349,195 @@ __device__ __forceinline__ void dispatch_small(const MoeArgs &a, const int *ids)
     a.sorted_row[P + i] = i;
     a.sorted_rank[P + i] = 0;
   }
+}
+
+// Stable counting sort of the P = N*K pairs by expert (pair order b*K + k), the order of
+// the reference's stable_sort (glm5_moe.cpp:191-200), over G workgroups of 16 waves:
+// workgroup g takes chunk g of the pairs, [g * cs, (g + 1) * cs), each of its waves a
+// segment of the chunk in pair order, 64 pairs at a time. Slot of a pair = the expert's
+// first slot + the pairs of that expert in earlier chunks (a.hist, G > 1), in earlier
+// segments of the chunk, and in earlier lanes of the round.
+struct DispatchChunk {
+  int c0, c1, seg;
+};
+__device__ __forceinline__ DispatchChunk dispatch_chunk(int P, int g) {
+  const int cs = (int)dispatch_chunk_pairs(P);
+  DispatchChunk ch;
+  ch.c0 = min(P, g * cs);
+  ch.c1 = min(P, ch.c0 + cs);
+  ch.seg = ((ch.c1 - ch.c0 + 15) / 16 + 63) / 64 * 64;
+  return ch;
+}
+
+// Per-wave counts of the chunk's pairs by expert into cnt[wave * kMaxE + e].
+__device__ __forceinline__ void chunk_counts(const MoeArgs &a, const int32_t *id_out, const DispatchChunk &ch,
+                                             int *cnt) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < 16 * kMaxE; i += 1024)
+    if ((i & (kMaxE - 1)) < a.E) cnt[i] = 0;
+  __syncthreads();
+  const int pbeg = ch.c0 + wave * ch.seg, pend = min(ch.c1, pbeg + ch.seg);
+  // A wave's pairs go 64 at a time; their experts are loaded kIdBatch rounds at once (the
+  // addresses clamped, so that no branch separates the loads): one memory round trip
+  // per batch instead of one per round.
+  for (int c0 = pbeg; c0 < pend; c0 += 64 * kIdBatch) {
+    int ev[kIdBatch];
+#pragma unroll
+    for (int q = 0; q < kIdBatch; ++q) ev[q] = id_out[min(c0 + 64 * q + lane, a.P - 1)];
+#pragma unroll
+    for (int q = 0; q < kIdBatch; ++q) {
+      if (c0 + 64 * q >= pend) break;
+      const int p = c0 + 64 * q + lane;
+      const bool valid = p < pend;
+      const int e = valid ? ev[q] : 0;
+      const uint64_t m = match_mask(e, valid);
+      if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  __syncthreads();
+}
+
+// Workgroup g of the dispatch: its chunk's per-wave counts; per expert the total and the
+// pairs of earlier chunks (from a.hist when G > 1); the expert bases and run / pass /
+// record indices by block scans (every workgroup computes the same ones); then the
+// scatter of its chunk. Workgroup 0 writes the run and pass tables; a run's record is
+// written by the workgroup that holds the run's first pair (it knows the run's first row).
+__device__ void dispatch_wg(const MoeArgs &a, const int32_t *id_out, int g, int G, int *cnt) {
+  __shared__ int s_run_of[kMaxE], s_base[kMaxE];  // per expert: its run record, its first slot
+  __shared__ int s_wv[16], s_wf[16], s_wg[16], s_wq[16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int E = a.E, K = a.topk, P = a.P;
+  const ExpertTab tab_t = a.tab[threadIdx.x < E ? threadIdx.x : 0];  // loaded during the count
+  const DispatchChunk ch = dispatch_chunk(P, g);
+  chunk_counts(a, id_out, ch, cnt);
+  // Per expert: total, pairs in earlier chunks, base offset (exclusive scan over experts),
+  // per-wave offsets.
+  const int t = threadIdx.x;
+  int tot = 0, pre = 0;
+  if (t < E) {
+    if (G == 1) {
+      for (int w = 0; w < 16; ++w) tot += cnt[w * kMaxE + t];
+    } else {
+      // the chunks' counts 8 at a time, all loads of a batch in flight together
+      for (int q0 = 0; q0 < G; q0 += 8) {
+        int h[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = a.hist[(int64_t)min(q0 + j, G - 1) * E + t];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int hj = q0 + j < G ? h[j] : 0;
+          tot += hj;
+          pre += q0 + j < g ? hj : 0;
+        }
+      }
+    }
+  }
+  // block exclusive scans of tot, of (tot > 0) and of the run's pass count (passes of
+  // at most kLongRows rows, the work units of the long-run expert kernels)
+  const int npass = (tot + kLongRows - 1) / kLongRows;
+  // runs that need several row passes of the short-run kernels go first in the run
+  // records, so that their longer workgroups start early instead of ending the launch
+  const int big = tot > a.pass_rows ? 1 : 0;
+  int v = tot, f = tot > 0 ? 1 : 0, gp = npass, q = big;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int ov = __shfl_up(v, d, 64), of = __shfl_up(f, d, 64), og = __shfl_up(gp, d, 64);
+    const int oq = __shfl_up(q, d, 64);
+    if (lane >= d) {
+      v += ov;
+      f += of;
+      gp += og;
+      q += oq;
+    }
+  }
+  if (lane == 63) {
+    s_wv[wave] = v;
+    s_wf[wave] = f;
+    s_wg[wave] = gp;
+    s_wq[wave] = q;
+  }
+  __syncthreads();
+  int pv = 0, pf = 0, pg = 0, pq = 0, nbig = 0;
+  for (int w = 0; w < 16; ++w) {
+    if (w < wave) {
+      pv += s_wv[w];
+      pf += s_wf[w];
+      pg += s_wg[w];
+      pq += s_wq[w];
+    }
+    nbig += s_wq[w];
+  }
+  const int base_e = pv + v - tot;           // exclusive
+  const int run_i = pf + f - (tot > 0 ? 1 : 0);
+  const int pass_i = pg + gp - npass;
+  const int big_i = pq + q - big;            // among the big runs
+  const int rec_i = big ? big_i : nbig + (run_i - big_i);  // big runs first, order kept
+  if (t < E) {
+    int run = base_e + pre;
+    for (int w = 0; w < 16; ++w) {
+      const int x = cnt[w * kMaxE + t];
+      cnt[w * kMaxE + t] = run;
+      run += x;
+    }
+    // the chunk that holds the expert's first pair writes its run record (row0 set by
+    // the scatter below)
+    if (pre == 0 && run > base_e) write_run_rec(a, rec_i, t, base_e, tot, 0, tab_t);
+    if (g == 0) {
+      if (tot > 0) {
+        a.run_expert[run_i] = t;
+        a.run_off[run_i] = base_e;
+        a.run_len[run_i] = tot;
+      }
+      for (int j = 0; j < npass; ++j) {
+        a.pass_expert[pass_i + j] = t;
+        a.pass_off[pass_i + j] = base_e + j * kLongRows;
+        a.pass_len[pass_i + j] = min(kLongRows, tot - j * kLongRows);
+      }
+    }
+    s_run_of[t] = rec_i;
+    s_base[t] = base_e;
+  }
+  if (g == 0 && t == 1023) {
+    int nrun = 0, npas = 0;
+    for (int w = 0; w < 16; ++w) {
+      nrun += s_wf[w];
+      npas += s_wg[w];
+    }
+    *a.n_runs = nrun;
+    *a.n_passes = npas;
+  }
+  __syncthreads();
+  const int pbeg = ch.c0 + wave * ch.seg, pend = min(ch.c1, pbeg + ch.seg);
+  for (int c0 = pbeg; c0 < pend; c0 += 64 * kIdBatch) {
+    int ev[kIdBatch];
+#pragma unroll
+    for (int qq = 0; qq < kIdBatch; ++qq) ev[qq] = id_out[min(c0 + 64 * qq + lane, P - 1)];
+#pragma unroll
+    for (int qq = 0; qq < kIdBatch; ++qq) {
+      if (c0 + 64 * qq >= pend) break;
+      const int p = c0 + 64 * qq + lane;
+      const bool valid = p < pend;
+      const int e = valid ? ev[qq] : 0;
+      const uint64_t m = match_mask(e, valid);
+      if (valid) {
+        const int pos = cnt[wave * kMaxE + e] + __builtin_popcountll(m & lanes_below());
+        a.sorted_row[pos] = p / K;
+        a.sorted_rank[pos] = p % K;
+        a.slot_e[pos] = e;
+        a.slot[p] = pos;
+        if (pos == s_base[e]) a.run_rec[s_run_of[e]].row0 = p / K;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  if (g == 0)
+    for (int i = threadIdx.x; i < a.N; i += 1024) {
+      a.sorted_row[P + i] = i;
+      a.sorted_rank[P + i] = 0;
+    }
 }
 
 // L2. Routing + dispatch. mode bit 0: top-k routing of rows blockIdx.x*16 + wave,
@@ -511,142 +710,27 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
     return;
   }
 
-  // Stable counting sort of the P = N*K pairs by expert (pair order b*K + k), the
-  // order of the reference's stable_sort (glm5_moe.cpp:191-200).
-  __shared__ int s_run_of[kMaxE], s_base[kMaxE];  // per expert: its run, its first slot
-  const ExpertTab tab_t = a.tab[threadIdx.x < E ? threadIdx.x : 0];  // loaded during the count
-  int *cnt = reinterpret_cast<int *>(&s_buf[0][0]);  // [16][kMaxE]
-  for (int i = threadIdx.x; i < 16 * kMaxE; i += 1024) cnt[i] = 0;
-  __syncthreads();
-  const int P = a.P;
-  const int seg = ((P + 15) / 16 + 63) / 64 * 64;
-  const int pbeg = wave * seg, pend = min(P, pbeg + seg);
-  // A wave's pairs go 64 at a time; their experts are loaded kIdBatch rounds at once (the
-  // addresses clamped, so that no branch separates the loads): one memory round trip
-  // per batch instead of one per round.
-  auto load_ids = [&](int c0, int (&ev)[kIdBatch]) {
+  // the one-workgroup form of the counting sort (the pairs as one chunk)
+  dispatch_wg(a, id_out, 0, 1, reinterpret_cast<int *>(&s_buf[0][0]));
+}
+
+// Dispatch of many pairs over G workgroups: k_moe_count writes each chunk's per-expert
+// counts to a.hist, then k_moe_dispatch (G workgroups again) scatters each chunk.
+__global__ __launch_bounds__(1024) void k_moe_count(MoeArgs a, const int32_t *id_out) {
+  __shared__ int cnt[16 * kMaxE];
+  const DispatchChunk ch = dispatch_chunk(a.P, blockIdx.x);
+  chunk_counts(a, id_out, ch, cnt);
+  for (int e = threadIdx.x; e < a.E; e += 1024) {
+    int t = 0;
 #pragma unroll
-    for (int q = 0; q < kIdBatch; ++q) ev[q] = id_out[min(c0 + 64 * q + lane, P - 1)];
-  };
-  for (int c0 = pbeg; c0 < pend; c0 += 64 * kIdBatch) {
-    int ev[kIdBatch];
-    load_ids(c0, ev);
-#pragma unroll
-    for (int q = 0; q < kIdBatch; ++q) {
-      if (c0 + 64 * q >= pend) break;
-      const int p = c0 + 64 * q + lane;
-      const bool valid = p < pend;
-      const int e = valid ? ev[q] : 0;
-      const uint64_t m = match_mask(e, valid);
-      if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
-      __builtin_amdgcn_wave_barrier();
-    }
+    for (int w = 0; w < 16; ++w) t += cnt[w * kMaxE + e];
+    a.hist[(int64_t)blockIdx.x * a.E + e] = t;
   }
-  __syncthreads();
-  // Per expert: total, base offset (exclusive scan over experts), per-wave offsets.
-  const int t = threadIdx.x;
-  int tot = 0;
-  if (t < E)
-    for (int w = 0; w < 16; ++w) tot += cnt[w * kMaxE + t];
-  // block exclusive scans of tot, of (tot > 0) and of the run's pass count (passes of
-  // at most kLongRows rows, the work units of the long-run expert kernels)
-  const int npass = (tot + kLongRows - 1) / kLongRows;
-  // runs that need several row passes of the short-run kernels go first in the run
-  // records, so that their longer workgroups start early instead of ending the launch
-  const int big = tot > a.pass_rows ? 1 : 0;
-  int v = tot, f = tot > 0 ? 1 : 0, g = npass, q = big;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int ov = __shfl_up(v, d, 64), of = __shfl_up(f, d, 64), og = __shfl_up(g, d, 64);
-    const int oq = __shfl_up(q, d, 64);
-    if (lane >= d) {
-      v += ov;
-      f += of;
-      g += og;
-      q += oq;
-    }
-  }
-  __shared__ int s_wv[16], s_wf[16], s_wg[16], s_wq[16];
-  if (lane == 63) {
-    s_wv[wave] = v;
-    s_wf[wave] = f;
-    s_wg[wave] = g;
-    s_wq[wave] = q;
-  }
-  __syncthreads();
-  int pv = 0, pf = 0, pg = 0, pq = 0, nbig = 0;
-  for (int w = 0; w < 16; ++w) {
-    if (w < wave) {
-      pv += s_wv[w];
-      pf += s_wf[w];
-      pg += s_wg[w];
-      pq += s_wq[w];
-    }
-    nbig += s_wq[w];
-  }
-  const int base_e = pv + v - tot;           // exclusive
-  const int run_i = pf + f - (tot > 0 ? 1 : 0);
-  const int pass_i = pg + g - npass;
-  const int big_i = pq + q - big;            // among the big runs
-  const int rec_i = big ? big_i : nbig + (run_i - big_i);  // big runs first, order kept
-  if (t < E) {
-    int run = base_e;
-    for (int w = 0; w < 16; ++w) {
-      const int x = cnt[w * kMaxE + t];
-      cnt[w * kMaxE + t] = run;
-      run += x;
-    }
-    if (tot > 0) {
-      a.run_expert[run_i] = t;
-      a.run_off[run_i] = base_e;
-      a.run_len[run_i] = tot;
-      write_run_rec(a, rec_i, t, base_e, tot, 0, tab_t);  // row0 set by the scatter below
-    }
-    s_run_of[t] = rec_i;
-    s_base[t] = base_e;
-    for (int j = 0; j < npass; ++j) {
-      a.pass_expert[pass_i + j] = t;
-      a.pass_off[pass_i + j] = base_e + j * kLongRows;
-      a.pass_len[pass_i + j] = min(kLongRows, tot - j * kLongRows);
-    }
-  }
-  if (t == 1023) {
-    int nrun = 0, npas = 0;
-    for (int w = 0; w < 16; ++w) {
-      nrun += s_wf[w];
-      npas += s_wg[w];
-    }
-    *a.n_runs = nrun;
-    *a.n_passes = npas;
-  }
-  __syncthreads();
-  for (int c0 = pbeg; c0 < pend; c0 += 64 * kIdBatch) {
-    int ev[kIdBatch];
-    load_ids(c0, ev);
-#pragma unroll
-    for (int q = 0; q < kIdBatch; ++q) {
-      if (c0 + 64 * q >= pend) break;
-      const int p = c0 + 64 * q + lane;
-      const bool valid = p < pend;
-      const int e = valid ? ev[q] : 0;
-      const uint64_t m = match_mask(e, valid);
-      if (valid) {
-        const int pos = cnt[wave * kMaxE + e] + __builtin_popcountll(m & lanes_below());
-        a.sorted_row[pos] = p / K;
-        a.sorted_rank[pos] = p % K;
-        a.slot_e[pos] = e;
-        a.slot[p] = pos;
-        if (pos == s_base[e]) a.run_rec[s_run_of[e]].row0 = p / K;
-      }
-      __builtin_amdgcn_wave_barrier();
-      if (valid && (__builtin_ctzll(m) == lane)) cnt[wave * kMaxE + e] += __builtin_popcountll(m);
-      __builtin_amdgcn_wave_barrier();
-    }
-  }
-  for (int i = threadIdx.x; i < a.N; i += 1024) {
-    a.sorted_row[P + i] = i;
-    a.sorted_rank[P + i] = 0;
-  }
+}
+
+__global__ __launch_bounds__(1024) void k_moe_dispatch(MoeArgs a, const int32_t *id_out, int G) {
+  __shared__ int cnt[16 * kMaxE];
+  dispatch_wg(a, id_out, blockIdx.x, G, cnt);
 }
 
 // ---------------------------------------------------------------------------------
@@ -881,7 +965,7 @@ namespace {
 struct MoeLayout {
   size_t total;
   size_t logits, weights, ids, sorted_row, sorted_rank, slot_e, slot, run_expert, run_off, run_len,
-      n_runs, run_rec, pass_expert, pass_off, pass_len, n_passes;
+      n_runs, run_rec, pass_expert, pass_off, pass_len, n_passes, hist;
   size_t yhat_gu, act, yhat_dn, dsh_gu, dsh_act, dsh_dn, xrot;
   int P, R, Imax, S_dn, max_passes;
 };
@@ -975,6 +1059,7 @@ MoeLayout moe_layout(const exl3_moe_layer_s *L, int64_t N) {
   m.pass_off = take(4 * (size_t)m.max_passes);
   m.pass_len = take(4 * (size_t)m.max_passes);
   m.n_passes = take(4);
+  m.hist = take(4 * (size_t)dispatch_wgs(m.P) * E);
   m.yhat_gu = take(4 * (size_t)slots * 2 * moe_slices(H) * m.Imax);
   m.act = take(2 * (size_t)slots * m.Imax);
   m.S_dn = std::max(moe_slices(I), SI > 0 ? moe_slices(SI) : 1);
@@ -1037,6 +1122,7 @@ MoeArgs make_args(const exl3_moe_layer_s *L, const MoeLayout &m, int64_t N, cons
   a.pass_off = (int32_t *)(ws + m.pass_off);
   a.pass_len = (int32_t *)(ws + m.pass_len);
   a.n_passes = (int32_t *)(ws + m.n_passes);
+  a.hist = (int32_t *)(ws + m.hist);
   a.yhat_gu = (float *)(ws + m.yhat_gu);
   a.act = (uint16_t *)(ws + m.act);
   a.yhat_dn = (float *)(ws + m.yhat_dn);
@@ -1073,7 +1159,15 @@ void launch_route(const MoeArgs &a, float *w_out, int32_t *id_out, int do_dispat
     } else {
       const unsigned g = (unsigned)std::min<int64_t>((a.N + 15) / 16, 4096);
       k_moe_route<J><<<g, 1024, 0, st>>>(a, w_out, id_out, 1);
-      if (do_dispatch) k_moe_route<J><<<1, 1024, 0, st>>>(a, w_out, id_out, 2);
+      if (do_dispatch) {
+        const int G = dispatch_wgs(a.P);
+        if (G == 1) {
+          k_moe_route<J><<<1, 1024, 0, st>>>(a, w_out, id_out, 2);
+        } else {
+          k_moe_count<<<G, 1024, 0, st>>>(a, id_out);
+          k_moe_dispatch<<<G, 1024, 0, st>>>(a, id_out, G);
+        }
+      }
     }
   });
 }

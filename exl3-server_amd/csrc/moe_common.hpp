@@ -100,6 +100,7 @@ struct MoeArgs {
   int32_t *pass_off;
   int32_t *pass_len;
   int32_t *n_passes;       // (1)
+  int32_t *hist;           // (G, E): per-chunk expert counts of a many-workgroup dispatch
   float *yhat_gu;      // (P + N, 2, S, Imax): gate/up k-slice partials (S slices of H)
                        // before the output Hadamard
   uint16_t *act;       // (P + N, Imax): rotated SwiGLU output per slot, MFMA k order

@@ -266,6 +266,41 @@ constexpr int kLongThreads = 512;
 constexpr int kStageBatchGu = 4;
 constexpr int kStageBatchDn = 4;
 
+// Stages one part of a pass's rows into LDS: rows [0, nr) of the source, row r at byte
+// r * row_bytes of `src` (a buffer resource that covers exactly those nr rows), their
+// 16-byte chunks [kbyte0 / 16, kbyte0 / 16 + q_row) into staged rows xs + r * xs_stride.
+// Thread t takes chunk t % q_row of rows t / q_row + j * (kLongThreads / q_row) (q_row a
+// power of two that divides kLongThreads), so that its source offset and LDS row only
+// step by whole rows; kBatch loads are issued before the first LDS store. A load of a row
+// at or past nr falls outside the resource and reads zero (no address clamps).
+template <bool kDup, int kBatch>
+__device__ __forceinline__ void stage_part(__amdgpu_buffer_rsrc_t src, uint32_t row_bytes, uint32_t kbyte0,
+                                           int q_row, int q_lg, int nr, uint32_t *xs, int xs_stride) {
+  // the thread's offsets are derived afresh at each call (the empty volatile asm keeps the
+  // compiler from hoisting them out of the slice loop, where they would hold VGPRs across
+  // the MFMA loop)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int cq = tid & (q_row - 1);
+  const int r0 = tid >> q_lg;
+  const int rstep = kLongThreads >> q_lg;
+  const uint32_t vstep = (uint32_t)rstep * row_bytes;
+  uint32_t vo = (uint32_t)r0 * row_bytes + (uint32_t)cq * 16 + kbyte0;
+  uint32_t *dst = xs + r0 * xs_stride;
+  const int dstep = rstep * xs_stride;
+  for (int r = r0; r < nr; r += kBatch * rstep) {
+    uint4 c[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q)
+      c[q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src, vo + q * vstep, 0, 0));
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q)
+      if (r + q * rstep < nr) stage_chunk<kDup>(dst + q * dstep, cq, c[q]);
+    vo += kBatch * vstep;
+    dst += kBatch * dstep;
+  }
+}
+
 // Work unit u of the long-run kernels: pass u of the dispatch's pass table, or (shared
 // mode) rows [u * kLongRows, u * kLongRows + kLongRows) of the trellis shared expert.
 __device__ __forceinline__ bool pass_info(const MoeArgs &a, int u, int shared_mode, RunInfo &ri) {
@@ -315,29 +350,18 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
 
   const int q_row = part_k / 8;  // 16-byte chunks of xrot per row and part (a power of two)
   const int q_lg = __builtin_ctz(q_row);
+  const uint32_t row_bytes = 4u * a.H;  // x_rot rows of a slot: gate's, then up's
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
+    // this projection's x_rot rows of the pass's slots (already rotated by k_moe_rotate,
+    // in the staged k order)
+    const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.xrot + ((int64_t)(ri.off + p0) * 2 + proj) * a.H), (short)0, (int)(nr * row_bytes), 0x00020000);
     f32x4 D[kLongBlocks][2];
     for (int sl = 0; sl < n_sl; ++sl) {
       for (int pt = 0; pt < n_parts; ++pt) {
-        // the part of the pass's rows, already rotated by k_moe_rotate (x_rot rows of
-        // this projection, in the staged k order)
         const int k0 = (sl * n_parts + pt) * part_k;
-        const int items = nr * q_row;
-        for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatchGu) {
-          uint4 c[kStageBatchGu];
-#pragma unroll
-          for (int q = 0; q < kStageBatchGu; ++q) {
-            const int i = min(i0 + q * kLongThreads, items - 1);
-            c[q] = reinterpret_cast<const uint4 *>(
-                a.xrot + ((int64_t)(ri.off + p0 + (i >> q_lg)) * 2 + proj) * a.H + k0)[i & (q_row - 1)];
-          }
-#pragma unroll
-          for (int q = 0; q < kStageBatchGu; ++q) {
-            const int i = i0 + q * kLongThreads;
-            if (i < items) stage_chunk<kDup>(xs + (i >> q_lg) * xs_stride, i & (q_row - 1), c[q]);
-          }
-        }
+        stage_part<kDup, kStageBatchGu>(src, row_bytes, 2u * k0, q_row, q_lg, nr, xs, xs_stride);
         __syncthreads();
         if (active)
           qmv_slice_rb<K, CB, PD, kLongBlocks>(base, k_tiles, out / 16, k0 / 16, np, part, xs, xs_stride,
@@ -390,27 +414,16 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   uint32_t *xs = smem;
   u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * slot_chunks(K);
 
+  const uint32_t row_bytes = 2u * a.Imax;
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
     const int nr = min(kLongRows, ri.len - p0);
+    const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.act + (int64_t)(ri.off + p0) * a.Imax), (short)0, (int)(nr * row_bytes), 0x00020000);
     f32x4 D[kLongBlocks][2];
     for (int sl = 0; sl < n_sl; ++sl) {
       for (int pt = 0; pt < n_parts; ++pt) {
         const int k0 = (sl * n_parts + pt) * part_k;
-        const int items = nr * q_row;  // 16-byte chunks of the part's rows
-        for (int i0 = threadIdx.x; i0 < items; i0 += kLongThreads * kStageBatchDn) {
-          uint4 c[kStageBatchDn];
-#pragma unroll
-          for (int q = 0; q < kStageBatchDn; ++q) {
-            const int i = min(i0 + q * kLongThreads, items - 1);
-            c[q] = reinterpret_cast<const uint4 *>(a.act + (int64_t)(ri.off + p0 + (i >> q_lg)) * a.Imax +
-                                                   k0)[i & (q_row - 1)];
-          }
-#pragma unroll
-          for (int q = 0; q < kStageBatchDn; ++q) {
-            const int i = i0 + q * kLongThreads;
-            if (i < items) stage_chunk<kDup>(xs + (i >> q_lg) * xs_stride, i & (q_row - 1), c[q]);
-          }
-        }
+        stage_part<kDup, kStageBatchDn>(src, row_bytes, 2u * k0, q_row, q_lg, nr, xs, xs_stride);
         __syncthreads();
         if (active)
           qmv_slice_rb<K, CB, PD, kLongBlocks>(tb.tr[2], k_tiles, a.H / 16, k0 / 16, np, part, xs, xs_stride,

@@ -552,15 +552,17 @@ def test_prefill_2048_config5(oracle, dev):
     d.close()
 
 
-def test_dispatch_many_pairs(oracle, dev):
-    # 2600 rows x top-8 = 20800 pairs: past 16384, so that each of the counting sort's
-    # waves takes its pairs' experts in two batches (16 rounds of 64, then 5), with hot
-    # experts whose runs need several 64-row passes; small tensors keep it quick
+@pytest.mark.parametrize("N", [2600, 8500])
+def test_dispatch_many_pairs(oracle, dev, N):
+    # the counting sort over several workgroups: 2600 rows x top-8 = 20800 pairs in 21
+    # chunks of 1024 (the last one ragged, 320 pairs); 8500 rows = 68000 pairs, past 64
+    # chunks of 1024, in 34 chunks of 2048 (two rounds of 64 pairs per wave); hot experts
+    # whose runs span chunks and need several 64-row passes; small tensors keep it quick
     cfg = synth.MoeConfig(hidden=256, inter=128, n_experts=64, top_k=8, routed_scaling_factor=2.0,
                           shared_inter=128, gate_up_K=3, gate_up_cb=1, down_K=2, down_cb=2, shared_K=0)
     hot = [3, 17, 40]
     layer, words = glm5_layer_on_device(dev, 61, "many", cfg, hot, 0.3)
-    N, H = 2600, cfg.hidden
+    H = cfg.hidden
     h = synth.activations(61, "many.x", N, H)
     x = to_dev(h, dev, N, 1, H)
     d = DeviceMoeLayer(layer, dev, words=words)
@@ -577,7 +579,7 @@ def test_dispatch_many_pairs(oracle, dev):
         hist[min(r, 64)] = hist.get(min(r, 64), 0) + 1
     assert d.diag()["run_hist"] == hist
     check_diag_bytes(d.diag(), runs["run_len"], cfg, LONG_PASS_ROWS)
-    rows = sorted(set(list(range(0, N, 157)) + [N - 1]))
+    rows = sorted(set(list(range(0, N, 157 if N < 4000 else 421)) + [N - 1]))
     yc = y.cpu()
     for r in rows:
         check_row_alone(d, x, yc, r, N)
