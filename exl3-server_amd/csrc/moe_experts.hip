@@ -318,6 +318,20 @@ __device__ __forceinline__ bool pass_info(const MoeArgs &a, int u, int shared_mo
   return true;
 }
 
+// Workgroup b of the long-run grid -> its work item: the workgroups of one pass (and the
+// passes of one expert, which follow each other) on one XCD, which then reads the pass's
+// rows and the expert's weights through its own L2. Workgroups go to the 8 XCDs in turn
+// (b % 8), each XCD taking its workgroups in b order; of the T live items [0, T), XCD
+// class x takes a contiguous range, item x * (T / 8) + min(x, T % 8) + b / 8. Returns -1
+// for b >= T (no work: the grid is sized for the most passes a call can have).
+__device__ __forceinline__ int long_item(int b, int per_unit, int shared_mode, const MoeArgs &a) {
+  const int units = shared_mode ? (a.N + kLongRows - 1) / kLongRows : *a.n_passes;
+  const int T = units * per_unit;
+  if (b >= T) return -1;
+  const int x = b & 7, q = T >> 3, r = T & 7;
+  return x * q + min(x, r) + (b >> 3);
+}
+
 template <int K, int CB, int PD>
 __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_moe_gate_up_long(MoeArgs a, int shared_mode, int dense_blocks) {
   extern __shared__ uint32_t smem[];
@@ -330,7 +344,8 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int out = shared_mode ? a.SI : a.I;
   const int n_np = out / 32, n_cb = (n_np + kWaves - 1) / kWaves;
   const int k_tiles = a.H / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
-  int b = blockIdx.x - dense_blocks;
+  int b = long_item(blockIdx.x - dense_blocks, 2 * n_cb, shared_mode, a);
+  if (b < 0) return;
   const int cb = b % n_cb;
   b /= n_cb;
   const int proj = b & 1, u = b >> 1;
@@ -397,7 +412,8 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int in = shared_mode ? a.SI : a.I;
   const int n_np = a.H / 32, n_cb = (n_np + kWaves - 1) / kWaves;
   const int k_tiles = in / 16, ss = slice_steps(k_tiles), n_sl = n_slices(k_tiles);
-  const int b = blockIdx.x - dense_blocks;
+  const int b = long_item(blockIdx.x - dense_blocks, n_cb, shared_mode, a);
+  if (b < 0) return;
   const int cb = b % n_cb, u = b / n_cb;
   RunInfo ri;
   if (!pass_info(a, u, shared_mode, ri)) return;
