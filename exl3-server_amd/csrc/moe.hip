@@ -754,32 +754,37 @@ __device__ __forceinline__ void down_out(float2 y, uint32_t sv, float &y0, float
   y1 = rf16(y1);
 }
 
-__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
+// kFold: a long-run call (one folded down partial per slot, a.fold). Its variant holds
+// few enough VGPRs for 7 waves per SIMD (the general one: 4), so that many more rows'
+// loads are in flight over a long call's many rows; the f16 shared expert's partials are
+// then loaded after the ranks.
+template <bool kFold>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFold ? 7 : 1))) void k_moe_combine(MoeArgs a) {
   const int lane = threadIdx.x & 63;
   const int n_cb = a.H / 128;
   const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (gw >= (int64_t)a.N * n_cb) return;
   const int row = (int)(gw / n_cb), cb = (int)(gw % n_cb);
   const int c = cb * 128 + 2 * lane;
-  const int n_sl = a.fold ? 1 : n_slices(a.I / 16);  // down partials per output
+  const int n_sl = kFold ? 1 : n_slices(a.I / 16);  // down partials per output
   const int64_t plane = a.H;  // floats between slice planes of one slot
   // the f16 shared expert's down partials (addresses known at entry): in flight with the
   // first round of the ranks' loads
   static_assert(kDenseSlots == 8, "two outputs' partials are four float4");
   float4 dsh[4];
-  if (a.shared_kind == exl3m::kSharedDense) {
+  auto load_dsh = [&] {
     const float4 *pd = reinterpret_cast<const float4 *>(a.dsh_dn + ((int64_t)row * a.H + c) * kDenseSlots);
 #pragma unroll
     for (int q = 0; q < 4; ++q) dsh[q] = pd[q];
-  }
+  };
+  if (!kFold && a.shared_kind == exl3m::kSharedDense) load_dsh();
   float r0 = 0.0f, r1 = 0.0f;
   for (int k0 = 0; k0 < a.topk; k0 += kCombineBatch) {
     const int nk = min(kCombineBatch, a.topk - k0);
     // three rounds of loads, each for all ranks of the batch at once (rank indices
     // clamped, so no branch separates them): pair -> slot/expert/weight -> the expert's
     // svh pointer -> svh words and the slot's down slice partials
-    int64_t slot[kCombineBatch];
-    int e[kCombineBatch];
+    int slot[kCombineBatch], e[kCombineBatch];
     float w[kCombineBatch];
 #pragma unroll
     for (int j = 0; j < kCombineBatch; ++j) {
@@ -788,27 +793,25 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
       e[j] = a.ids[pk];
       w[j] = a.weights[pk];
     }
-    const uint16_t *svp[kCombineBatch];
-#pragma unroll
-    for (int j = 0; j < kCombineBatch; ++j) svp[j] = a.svh_s[2] + (int64_t)e[j] * a.H;
+    const uint16_t *svb = a.svh_s[2] + c;
     uint32_t sv[kCombineBatch];
     float2 y[kCombineBatch];
-    if (n_sl == 1) {
+    if (kFold || n_sl == 1) {
       // long-run calls: one folded partial per slot
 #pragma unroll
       for (int j = 0; j < kCombineBatch; ++j) {
-        sv[j] = *reinterpret_cast<const uint32_t *>(svp[j] + c);
-        y[j] = *reinterpret_cast<const float2 *>(a.yhat_dn + slot[j] * a.S_dn * plane + c);
+        sv[j] = *reinterpret_cast<const uint32_t *>(svb + (int64_t)e[j] * a.H);
+        y[j] = *reinterpret_cast<const float2 *>(a.yhat_dn + (int64_t)slot[j] * a.S_dn * plane + c);
       }
     } else if (n_sl <= kCombineSlices) {
       float2 part[kCombineBatch][kCombineSlices];
 #pragma unroll
       for (int j = 0; j < kCombineBatch; ++j) {
-        sv[j] = *reinterpret_cast<const uint32_t *>(svp[j] + c);
+        sv[j] = *reinterpret_cast<const uint32_t *>(svb + (int64_t)e[j] * a.H);
 #pragma unroll
         for (int q = 0; q < kCombineSlices; ++q)
           part[j][q] = *reinterpret_cast<const float2 *>(
-              a.yhat_dn + (slot[j] * a.S_dn + min(q, n_sl - 1)) * plane + c);
+              a.yhat_dn + ((int64_t)slot[j] * a.S_dn + min(q, n_sl - 1)) * plane + c);
       }
 #pragma unroll
       for (int j = 0; j < kCombineBatch; ++j) {
@@ -823,24 +826,30 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     } else {
 #pragma unroll
       for (int j = 0; j < kCombineBatch; ++j) {
-        sv[j] = *reinterpret_cast<const uint32_t *>(svp[j] + c);
-        y[j] = exl3m::ordered_sum2<4>(a.yhat_dn + slot[j] * a.S_dn * plane + c, plane, n_sl);
+        sv[j] = *reinterpret_cast<const uint32_t *>(svb + (int64_t)e[j] * a.H);
+        y[j] = exl3m::ordered_sum2<4>(a.yhat_dn + (int64_t)slot[j] * a.S_dn * plane + c, plane, n_sl);
       }
     }
-    float v0[kCombineBatch], v1[kCombineBatch], s0[kCombineBatch], s1[kCombineBatch];
+    // the output Hadamards kHadGroup ranks at a time (their stages interleaved), in rank
+    // order into the sums
+    constexpr int kHadGroup = kFold ? 4 : kCombineBatch;
 #pragma unroll
-    for (int j = 0; j < kCombineBatch; ++j) {
-      v0[j] = y[j].x;
-      v1[j] = y[j].y;
-      s0[j] = lo16(sv[j]);
-      s1[j] = hi16(sv[j]);
-    }
-    wave_had_post_n<kCombineBatch>(v0, v1, s0, s1);
+    for (int g0 = 0; g0 < kCombineBatch; g0 += kHadGroup) {
+      float v0[kHadGroup], v1[kHadGroup], s0[kHadGroup], s1[kHadGroup];
 #pragma unroll
-    for (int j = 0; j < kCombineBatch; ++j) {
-      if (j < nk) {
-        r0 += rf16(rf16(v0[j]) * w[j]);
-        r1 += rf16(rf16(v1[j]) * w[j]);
+      for (int j = 0; j < kHadGroup; ++j) {
+        v0[j] = y[g0 + j].x;
+        v1[j] = y[g0 + j].y;
+        s0[j] = lo16(sv[g0 + j]);
+        s1[j] = hi16(sv[g0 + j]);
+      }
+      wave_had_post_n<kHadGroup>(v0, v1, s0, s1);
+#pragma unroll
+      for (int j = 0; j < kHadGroup; ++j) {
+        if (g0 + j < nk) {
+          r0 += rf16(rf16(v0[j]) * w[g0 + j]);
+          r1 += rf16(rf16(v1[j]) * w[g0 + j]);
+        }
       }
     }
   }
@@ -848,13 +857,15 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   r1 = rf16(r1);
   if (a.shared_kind == exl3m::kSharedTrellis) {
     const int64_t slot = (int64_t)a.P + row;
-    const float2 ys = exl3m::ordered_sum2<4>(a.yhat_dn + slot * a.S_dn * plane + c, plane,
-                                             a.fold ? 1 : n_slices(a.SI / 16));
+    const float2 ys = kFold ? *reinterpret_cast<const float2 *>(a.yhat_dn + slot * a.S_dn * plane + c)
+                            : exl3m::ordered_sum2<4>(a.yhat_dn + slot * a.S_dn * plane + c, plane,
+                                                     n_slices(a.SI / 16));
     float y0, y1;
     down_out(ys, *reinterpret_cast<const uint32_t *>(a.svh_s[2] + (int64_t)a.E * a.H + c), y0, y1);
     r0 += y0;
     r1 += y1;
   } else if (a.shared_kind == exl3m::kSharedDense) {
+    if (kFold) load_dsh();
     // dense_slots_sum's order over the two outputs' kDenseSlots partials
     const int S = dense_mfma_splits(a.SI);
     const float v0[8] = {dsh[0].x, dsh[0].y, dsh[0].z, dsh[0].w, dsh[1].x, dsh[1].y, dsh[1].z, dsh[1].w};
@@ -1826,7 +1837,10 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
     if (rc) return rc;
   }
   // L6: combine
-  k_moe_combine<<<(unsigned)((N * (H / 128) + 3) / 4), 256, 0, st>>>(a);
+  if (a.fold)
+    k_moe_combine<true><<<(unsigned)((N * (H / 128) + 3) / 4), 256, 0, st>>>(a);
+  else
+    k_moe_combine<false><<<(unsigned)((N * (H / 128) + 3) / 4), 256, 0, st>>>(a);
   EXL3_LAUNCHED("k_moe_combine");
   if (timed) {
     EXL3_HIP(hipEventRecord(layer->ev[4], st));
