@@ -981,9 +981,10 @@ struct MoeLayout {
   int P, R, Imax, S_dn, max_passes;
 };
 
-// Calls of at least this many token rows take the long-run expert kernels (outputs are
-// bit-identical either way): EXL3_MOE_LONG_ROWS, read once, default 65 (at 64 rows the
-// slice-parallel short-run kernels are still faster).
+// Calls of at least this many token rows take the long-run expert kernels (one
+// accumulator chain over the whole k range: within the reference's staged-path bound of
+// the short-run path, not bit-identical to it): EXL3_MOE_LONG_ROWS, read once, default 65
+// (at 64 rows the slice-parallel short-run kernels are still faster).
 int64_t long_min_rows() {
   static const int64_t v = [] {
     const char *e = std::getenv("EXL3_MOE_LONG_ROWS");

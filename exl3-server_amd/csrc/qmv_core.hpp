@@ -428,9 +428,8 @@ __device__ __forceinline__ void mfma_quad_rb(const uint32_t (&W)[K + 1], const u
 
 // Long runs: RB blocks of 16 token rows share one decode. The B operands of a wave step
 // are decoded once and each block b runs the step's MFMAs with its own A operands
-// (staged row 16b + l%16 at word offset xo[b] of xs) and accumulators; per block the
-// accumulation is exactly mfma_step's, so every row's result is bit-identical to a
-// 16-row pass.
+// (staged row 16b + l%16 at word offset xo[b] of xs) and accumulators; per block a
+// step's MFMAs are exactly mfma_step's (the same operands in the same order).
 template <int K, int CB, int RB>
 __device__ __forceinline__ void mfma_step_rb(const uint32_t (&W)[K + 1], const uint32_t *xs,
                                              const int (&xo)[RB], f32x4 (&D)[RB][2]) {

@@ -139,8 +139,9 @@ def halves_sum_lut(cb: int) -> np.ndarray:
 
 class gemv_mode:
     """Context manager: the oracle's GEMV weights inside the block. exact_halves=True
-    uses the unrounded lo + hi sum for mcg/3inst (the value the GPU GEMV multiplies),
-    False the reference's f16 weights (the default)."""
+    uses the unrounded lo + hi sum for mcg/3inst (the value the GPU's exact-halves form
+    multiplies), False the reference's f16 weights (the default, and the GPU's default
+    form)."""
 
     def __init__(self, exact_halves: bool):
         self.mode = 1 if exact_halves else 0
