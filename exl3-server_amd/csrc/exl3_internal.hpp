@@ -77,7 +77,7 @@ exl3_status launch_qmv_finalize(int n, int n_sl, int64_t rows, int out, const fl
 // and the two launches (projection partials, then finalize with the optional RMSNorm).
 exl3_status check_hc(const exl3_hc_site *hc, int D);
 inline exl3_status check_hc_shape(int n, int D) {
-  return (n < 1 || n > 4 || D <= 0 || D > 8192 || D % 2 || ((int64_t)n * D) % 64) ? EXL3_ERR_UNSUPPORTED : EXL3_OK;
+  return (n < 1 || n > 8 || D <= 0 || D > 8192 || D % 2 || ((int64_t)n * D) % 64) ? EXL3_ERR_UNSUPPORTED : EXL3_OK;
 }
 size_t hc_part_bytes(int N, int D, int64_t P);
 // Whether two buffers of n bytes each share a byte.

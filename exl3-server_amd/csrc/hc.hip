@@ -3,7 +3,7 @@
 // collapsed stream (rms_norm, glm5_attn.cpp:12-22) and the hyper-connection mix
 // (g5_hc_mix, glm5_hc.cpp:342-355), gfx950.
 //
-//  k_hc_proj      grid (k chunk of the N*D axis, group of kHcRows positions): per position
+//  k_hc_proj      grid (k chunk of the N*D axis, group of positions): per position
 //                 the chunk's sum of squares and its part of the W = (2+N)*N projections
 //                 x . fn[j] (fn stored (W, N*D), as the reference's F.linear weight);
 //                 f32 partials per chunk. Each wave keeps its projections' fn slice in
@@ -32,11 +32,26 @@ using namespace exl3d;
 
 namespace {
 
-constexpr int kHcMaxN = 4;                       // streams (W <= 24), as the reference's fused path
-constexpr int kHcMaxW = (2 + kHcMaxN) * kHcMaxN;
+constexpr int kHcMaxN = 8;                       // streams (W <= 80)
+constexpr int kHcNarrowN = 4;                    // the narrow kernels' streams (W <= 24; GLM-5's 4)
 constexpr int kHcChunk = 64;                     // elements of the N*D axis per workgroup
-constexpr int kHcRows = 8;                       // positions per projection workgroup
-constexpr int kHcVals = kHcMaxW + 1;             // per chunk: W projections, then the sum of squares
+
+// Per kernel variant (kN = 4: 1..4 streams; kN = 8: 5..8): the W = (2+N)*N projections'
+// bound, the values per (position, chunk) partial (the W projections, then the sum of
+// squares, at index kMaxW), positions per projection workgroup, and the finalize's
+// reduction of the chunk partials by kG groups of kJ threads.
+template <int kN>
+struct HcShape {
+  static constexpr int kMaxW = (2 + kN) * kN;
+  static constexpr int kVals = kMaxW + 1;
+  static constexpr int kRows = kN <= kHcNarrowN ? 8 : 3;
+  static constexpr int kProjThreads = kVals * kRows;  // 200, 243
+  static constexpr int kJ = kN <= kHcNarrowN ? 32 : 128;
+  static constexpr int kG = 256 / kJ;
+  static_assert(kProjThreads <= 256 && kVals <= kJ, "hc shape");
+};
+// Values per (position, chunk) partial for N streams (the part buffer's layout).
+constexpr int hc_vals(int N) { return N <= kHcNarrowN ? HcShape<kHcNarrowN>::kVals : HcShape<kHcMaxN>::kVals; }
 
 __device__ __forceinline__ float wave_sum(float v) {
   v += xor_lanes<1>(v);
@@ -50,20 +65,20 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ float h2f(uint16_t v) { return (float)bitcast<f16>(v); }
 
-// Thread (j, r): projection j < W of position p0 + r (r < kHcRows), the dot product of
+// Thread (j, r): projection j < W of position p0 + r (r < kRows), the dot product of
 // the workgroup's chunk of the N*D axis with fn row j, in k order; threads past the
 // projections: the chunk's sum of squares of position p0 + r. All of a thread's loads are
 // in flight at once; no cross-lane reduction.
-constexpr int kHcProjThreads = (kHcMaxW + 1) * kHcRows;  // 200
-
+template <int kN>
 __global__ __launch_bounds__(256) void k_hc_proj(const uint16_t *__restrict__ streams, int64_t P, int ND, int W,
                                                  const float *__restrict__ fn, float *__restrict__ part) {
+  using S = HcShape<kN>;
   const int chunk = blockIdx.x, n_chunks = gridDim.x;
   const int t = threadIdx.x;
-  if (t >= kHcProjThreads) return;
-  const bool sq = t >= kHcMaxW * kHcRows;
-  const int j = sq ? kHcMaxW : t / kHcRows, r = t % kHcRows;
-  const int64_t p = (int64_t)blockIdx.y * kHcRows + r;
+  if (t >= S::kProjThreads) return;
+  const bool sq = t >= S::kMaxW * S::kRows;
+  const int j = sq ? S::kMaxW : t / S::kRows, r = t % S::kRows;
+  const int64_t p = (int64_t)blockIdx.y * S::kRows + r;
   if (p >= P || (!sq && j >= W)) return;
   const int k0 = chunk * kHcChunk;
   const uint16_t *s = streams + p * ND + k0;
@@ -96,7 +111,7 @@ __global__ __launch_bounds__(256) void k_hc_proj(const uint16_t *__restrict__ st
       }
     }
   }
-  part[(p * n_chunks + chunk) * kHcVals + j] = acc;
+  part[(p * n_chunks + chunk) * S::kVals + j] = acc;
 }
 
 // Sum of one value over a workgroup of 4 waves, the waves' sums added in wave order.
@@ -146,65 +161,110 @@ __device__ __forceinline__ void rms_pairs(const float (&x0)[kHcPairs], const flo
     }
 }
 
+template <int kN>
 __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict__ streams, int N, int D, int W,
                                                      int n_chunks, const float *__restrict__ part,
                                                      const float *__restrict__ base, const float *__restrict__ scale,
                                                      int iters, float eps, const uint16_t *__restrict__ norm_w,
                                                      float norm_eps, uint16_t *__restrict__ out,
                                                      float *__restrict__ post_out, float *__restrict__ comb_out) {
-  __shared__ float vals[kHcVals];
-  __shared__ float grp[8][32];
-  __shared__ float pre[kHcMaxN];
+  using S = HcShape<kN>;
+  constexpr bool kNarrow = kN <= kHcNarrowN;
+  __shared__ float vals[S::kVals];
+  __shared__ float grp[S::kG][S::kJ];
+  __shared__ float pre[kN];
   __shared__ float red[4];
   const int64_t p = blockIdx.x;
   const int64_t ND = (int64_t)N * D;
   const int t = threadIdx.x;
-  // the row's stream pairs, in flight while the projections are finished
+  // the row's stream pairs, in flight while the projections are finished (the narrow
+  // variant; the wide one loads each stream at the collapse, to keep its registers)
   const uint16_t *srow = streams + p * ND;
-  uint32_t sp[kHcMaxN][kHcPairs];
+  uint32_t sp[kNarrow ? kN : 1][kHcPairs];
+  if constexpr (kNarrow) {
 #pragma unroll
-  for (int n = 0; n < kHcMaxN; ++n)
+    for (int n = 0; n < kN; ++n)
 #pragma unroll
-    for (int i = 0; i < kHcPairs; ++i)
-      sp[n][i] = n < N && pair_d(i) < D ? *reinterpret_cast<const uint32_t *>(srow + (int64_t)n * D + pair_d(i))
-                                        : 0u;
+      for (int i = 0; i < kHcPairs; ++i)
+        sp[n][i] = n < N && pair_d(i) < D ? *reinterpret_cast<const uint32_t *>(srow + (int64_t)n * D + pair_d(i))
+                                          : 0u;
+  }
   // the norm weights too (the row's own streams stand in when there is no norm: same
   // length, never used)
   uint32_t wv[kHcPairs];
   load_pairs(norm_w ? norm_w : srow, D, wv);
-  // the chunk partials: thread (g, j) sums value j over chunks g, g + 8, ... in order
-  // (their loads in flight together), then value j is the sum of the 8 group sums in
+  // the chunk partials: thread (g, j) sums value j over chunks g, g + kG, ... in order
+  // (their loads in flight together), then value j is the sum of the kG group sums in
   // group order
   {
-    const int j = t & 31, g = t >> 5;
+    const int j = t % S::kJ, g = t / S::kJ;
     float acc = 0.0f;
-    if (j < W || j == kHcMaxW) {
-      const float *pp = part + p * n_chunks * kHcVals + j;
-      for (int c0 = g; c0 < n_chunks; c0 += 8 * 32) {
+    if (j < W || j == S::kMaxW) {
+      const float *pp = part + p * n_chunks * S::kVals + j;
+      for (int c0 = g; c0 < n_chunks; c0 += S::kG * 32) {
         float v[32];
 #pragma unroll
-        for (int q = 0; q < 32; ++q) v[q] = pp[(int64_t)min(c0 + 8 * q, n_chunks - 1) * kHcVals];
+        for (int q = 0; q < 32; ++q) v[q] = pp[(int64_t)min(c0 + S::kG * q, n_chunks - 1) * S::kVals];
 #pragma unroll
         for (int q = 0; q < 32; ++q)
-          if (c0 + 8 * q < n_chunks) acc += v[q];
+          if (c0 + S::kG * q < n_chunks) acc += v[q];
       }
     }
     grp[g][j] = acc;
   }
   __syncthreads();
-  if (t < W || t == kHcMaxW) {
+  if (t < W || t == S::kMaxW) {
     float acc = grp[0][t];
 #pragma unroll
-    for (int g = 1; g < 8; ++g) acc += grp[g][t];
+    for (int g = 1; g < S::kG; ++g) acc += grp[g][t];
     vals[t] = acc;
   }
   __syncthreads();
-  if (t < 64) {
+  if (t < 64 && !kNarrow) {
+    // wave 0, the wide variant: lane l holds comb entry (l / 8, l % 8) of an 8 x 8
+    // layout (entries outside N x N stay 0): a row is 8 consecutive lanes, a column the
+    // lanes 8 apart; sums by lane exchanges at distances 1, 2, 4 (rows) and 8, 16, 32
+    // (columns)
+    const float rms = 1.0f / sqrtf(vals[S::kMaxW] / (float)ND + eps);
+    const int lane = t;
+    if (lane < N) {
+      const float wp = vals[lane] * rms, wq = vals[N + lane] * rms;
+      pre[lane] = 1.0f / (1.0f + expf(-(wp * scale[0] + base[lane]))) + eps;
+      post_out[p * N + lane] = 2.0f * (1.0f / (1.0f + expf(-(wq * scale[1] + base[N + lane]))));
+    }
+    const int ci = lane >> 3, cj = lane & 7;
+    const bool live = ci < N && cj < N;
+    auto row_sum = [&](float v) {
+      const float s = v + xor_lanes<1>(v);
+      const float s2 = s + xor_lanes<2>(s);
+      return s2 + xor_lanes<4>(s2);
+    };
+    auto col_sum = [&](float v) {
+      const float s = v + xor_lanes<8>(v);
+      const float s2 = s + xor_lanes<16>(s);
+      return s2 + xor_lanes<32>(s2);
+    };
+    const float z = live ? vals[2 * N + ci * N + cj] * rms * scale[2] + base[2 * N + ci * N + cj] : -INFINITY;
+    float m = fmaxf(z, xor_lanes<1>(z));
+    m = fmaxf(m, xor_lanes<2>(m));
+    m = fmaxf(m, xor_lanes<4>(m));
+    float c = live ? expf(z - m) : 0.0f;
+    const float rs = row_sum(c);
+    c = live ? c / rs + eps : 0.0f;
+    auto norm = [&](float v, float sum) { return live ? v / (sum + eps) : 0.0f; };
+    c = norm(c, col_sum(c));
+    for (int it = 0; it < iters - 1; ++it) {
+      c = norm(c, row_sum(c));
+      c = norm(c, col_sum(c));
+    }
+    if (live) comb_out[p * N * N + ci * N + cj] = c;
+  }
+  if (t < 64 && kNarrow) {
     // wave 0: lane l < 16 holds comb entry (l / 4, l % 4) of a 4 x 4 layout (entries
     // outside N x N stay 0), so a row is a quad and a column the lanes j, j + 4, j + 8,
     // j + 12 of the first 16: row sums by quad-permute DPP, column sums by row-rotate DPP,
     // no LDS round trip per reduction
-    const float rms = 1.0f / sqrtf(vals[kHcMaxW] / (float)ND + eps);
+    const float rms = 1.0f / sqrtf(vals[S::kMaxW] / (float)ND + eps);
     const int lane = t;
     if (lane < N) {
       const float wp = vals[lane] * rms, wq = vals[N + lane] * rms;
@@ -250,17 +310,39 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
   __syncthreads();
   // collapsed = sum_n pre[n] * streams[n], in f16
   float x0[kHcPairs], x1[kHcPairs];
+  if constexpr (kNarrow) {
 #pragma unroll
-  for (int i = 0; i < kHcPairs; ++i) {
-    float a0 = 0.0f, a1 = 0.0f;
+    for (int i = 0; i < kHcPairs; ++i) {
+      float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-    for (int n = 0; n < kHcMaxN; ++n)
-      if (n < N) {
-        a0 = fmaf(pre[n], h2f(sp[n][i] & 0xffff), a0);
-        a1 = fmaf(pre[n], h2f(sp[n][i] >> 16), a1);
+      for (int n = 0; n < kN; ++n)
+        if (n < N) {
+          a0 = fmaf(pre[n], h2f(sp[n][i] & 0xffff), a0);
+          a1 = fmaf(pre[n], h2f(sp[n][i] >> 16), a1);
+        }
+      x0[i] = (float)to_f16(a0);
+      x1[i] = (float)to_f16(a1);
+    }
+  } else {
+    // stream by stream (the same fma chain per element, n ascending)
+#pragma unroll
+    for (int i = 0; i < kHcPairs; ++i) x0[i] = x1[i] = 0.0f;
+    for (int n = 0; n < N; ++n) {
+      uint32_t v[kHcPairs];
+#pragma unroll
+      for (int i = 0; i < kHcPairs; ++i)
+        v[i] = *reinterpret_cast<const uint32_t *>(srow + (int64_t)n * D + min(pair_d(i), D - 2));
+#pragma unroll
+      for (int i = 0; i < kHcPairs; ++i) {
+        x0[i] = fmaf(pre[n], h2f(v[i] & 0xffff), x0[i]);
+        x1[i] = fmaf(pre[n], h2f(v[i] >> 16), x1[i]);
       }
-    x0[i] = (float)to_f16(a0);
-    x1[i] = (float)to_f16(a1);
+    }
+#pragma unroll
+    for (int i = 0; i < kHcPairs; ++i) {
+      x0[i] = (float)to_f16(x0[i]);
+      x1[i] = (float)to_f16(x1[i]);
+    }
   }
   if (!norm_w) {
 #pragma unroll
@@ -311,7 +393,7 @@ namespace exl3h {
 exl3_status check_hc(const exl3_hc_site *hc, int D) {
   if (!hc || !hc->fn || !hc->base || !hc->scale) return fail(EXL3_ERR_INVALID, "null hyper-connection site");
   if (hc->mult < 1 || hc->mult > kHcMaxN)
-    return fail(EXL3_ERR_UNSUPPORTED, "hc_mult must be 1..4 (the fused path's range)");
+    return fail(EXL3_ERR_UNSUPPORTED, "hc_mult must be 1..8");
   if (hc->sinkhorn_iters < 1) return fail(EXL3_ERR_INVALID, "hc_sinkhorn_iters must be >= 1");
   if (D <= 0 || D > kHcMaxD || D % 2 || ((int64_t)hc->mult * D) % kHcChunk)
     return fail(EXL3_ERR_UNSUPPORTED, "hidden size must be even, at most 8192, and N*hidden a multiple of 64");
@@ -319,21 +401,32 @@ exl3_status check_hc(const exl3_hc_site *hc, int D) {
 }
 
 size_t hc_part_bytes(int N, int D, int64_t P) {
-  return align_up((size_t)P * ((size_t)N * D / kHcChunk) * kHcVals * 4, 256);
+  return align_up((size_t)P * ((size_t)N * D / kHcChunk) * hc_vals(N) * 4, 256);
+}
+
+template <int kN>
+static void hc_prepare_go(const exl3_hc_site *hc, const uint16_t *streams, int64_t P, int D, int64_t groups,
+                          const uint16_t *norm_w, float norm_eps, uint16_t *out, float *post, float *comb,
+                          float *part, hipStream_t st) {
+  const int N = hc->mult, W = (2 + N) * N, ND = N * D, n_chunks = ND / kHcChunk;
+  k_hc_proj<kN><<<dim3((unsigned)n_chunks, (unsigned)groups), 256, 0, st>>>(streams, P, ND, W, hc->fn, part);
+  k_hc_finalize<kN><<<(unsigned)P, 256, 0, st>>>(streams, N, D, W, n_chunks, part, hc->base, hc->scale,
+                                                  hc->sinkhorn_iters, hc->eps, norm_w, norm_eps, out, post, comb);
 }
 
 exl3_status launch_hc_prepare(const exl3_hc_site *hc, const uint16_t *streams, int64_t P, int D,
                               const uint16_t *norm_w, float norm_eps, uint16_t *out, float *post,
                               float *comb, float *part, hipStream_t st) {
-  const int N = hc->mult, W = (2 + N) * N, ND = N * D, n_chunks = ND / kHcChunk;
   if (P == 0) return EXL3_OK;
-  const int64_t groups = (P + kHcRows - 1) / kHcRows;
+  const bool narrow = hc->mult <= kHcNarrowN;
+  const int rows = narrow ? HcShape<kHcNarrowN>::kRows : HcShape<kHcMaxN>::kRows;
+  const int64_t groups = (P + rows - 1) / rows;
   if (groups > 65535) return fail(EXL3_ERR_UNSUPPORTED, "too many positions in one call");
-  k_hc_proj<<<dim3((unsigned)n_chunks, (unsigned)groups), 256, 0, st>>>(streams, P, ND, W, hc->fn, part);
-  EXL3_LAUNCHED("k_hc_proj");
-  k_hc_finalize<<<(unsigned)P, 256, 0, st>>>(streams, N, D, W, n_chunks, part, hc->base, hc->scale,
-                                              hc->sinkhorn_iters, hc->eps, norm_w, norm_eps, out, post, comb);
-  EXL3_LAUNCHED("k_hc_finalize");
+  if (narrow)
+    hc_prepare_go<kHcNarrowN>(hc, streams, P, D, groups, norm_w, norm_eps, out, post, comb, part, st);
+  else
+    hc_prepare_go<kHcMaxN>(hc, streams, P, D, groups, norm_w, norm_eps, out, post, comb, part, st);
+  EXL3_LAUNCHED("k_hc_proj / k_hc_finalize");
   return EXL3_OK;
 }
 
@@ -384,7 +477,7 @@ exl3_status exl3_rms_norm(const uint16_t *x, int64_t P, int32_t hidden, const ui
 exl3_status exl3_hc_mix(const uint16_t *block_out, const float *post, const float *comb, const uint16_t *residual,
                         int64_t P, int32_t mult, int32_t hidden, uint16_t *out, exl3_stream_t stream) {
   if (P < 0 || mult < 1 || mult > kHcMaxN || hidden <= 0 || hidden % 2)
-    return fail(EXL3_ERR_INVALID, "exl3_hc_mix: bad shape (hc_mult 1..4, even hidden)");
+    return fail(EXL3_ERR_INVALID, "exl3_hc_mix: bad shape (hc_mult 1..8, even hidden)");
   if (P == 0) return EXL3_OK;
   if (!block_out || !post || !comb || !residual || !out) return fail(EXL3_ERR_INVALID, "exl3_hc_mix: null argument");
   if ((reinterpret_cast<uintptr_t>(block_out) | reinterpret_cast<uintptr_t>(residual) |

@@ -712,7 +712,7 @@ exl3_status exl3_moe_layer_load_block(exl3_moe_layer_t layer, const char *const 
   if (!layer || !shard_paths || n_shards <= 0 || !layer_prefix || !site || !norm_w)
     return fail(EXL3_ERR_INVALID, "exl3_moe_layer_load_block: bad arguments");
   const int N = site->mult, D = layer_hidden(layer);
-  if (N < 1 || N > 4) return fail(EXL3_ERR_UNSUPPORTED, "hc_mult must be 1..4 (the fused path's range)");
+  if (N < 1 || N > 8) return fail(EXL3_ERR_UNSUPPORTED, "hc_mult must be 1..8");
   Loader L;
   L.st = stream_of(stream);
   struct Closer {

@@ -1643,7 +1643,7 @@ BlockLayout block_layout(exl3_moe_layer_t layer, int n, int64_t P, const MoeLayo
 }  // namespace
 
 size_t exl3_moe_block_workspace_size(exl3_moe_layer_t layer, int32_t hc_mult, int64_t P) {
-  if (!layer || P < 0 || hc_mult < 1 || hc_mult > 4 || check_hc_shape(hc_mult, layer->H)) return 0;
+  if (!layer || P < 0 || hc_mult < 1 || hc_mult > 8 || check_hc_shape(hc_mult, layer->H)) return 0;
   if (P == 0) return 0;
   if (P > (1 << 24) / layer->topk) return 0;
   return block_layout(layer, hc_mult, P, moe_layout(layer, P)).total;

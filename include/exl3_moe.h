@@ -322,7 +322,8 @@ exl3_status exl3_moe_diag_reset(exl3_moe_layer_t layer);
 /* One hyper-connection site (G5Layer hc_ffn_* / hc_attn_*, glm5.h:79-82; config
  * hc_mult, hc_sinkhorn_iters, hc_eps, model.h:65-67). fn is (W, mult*hidden) f32 with
  * W = (2 + mult) * mult, stored (out, in) as F.linear's weight; base (W) f32; scale (3)
- * f32. mult 1..4 (the reference's fused kernel's range). */
+ * f32. mult 1..8 (the reference's fused kernel takes 1..4 and its MLX expression any
+ * count; GLM-5 uses 4). */
 typedef struct {
   int32_t mult;
   int32_t sinkhorn_iters;

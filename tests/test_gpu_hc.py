@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 EPS = 1e-6           # GLM-5 hc_eps
 NORM_EPS = 1e-5      # GLM-5 rms_norm_eps
 MISMATCH_FRAC = 1e-2
-COND = 1e-6          # f32 round-off of pre[n] and of the 4-term sum, relative to the terms
+COND = 1e-6          # f32 round-off of pre[n] and of the N-term sum, relative to the terms
 TOL_RMS = 2e-2
 COS_MIN = 0.9999
 
@@ -73,7 +73,10 @@ def collapse_cond(st_bits):
     return COND * np.abs(st_bits.view(np.float16).astype(np.float64)).sum(1)
 
 
-SHAPES = [(8, 4, 4096), (3, 4, 512), (5, 2, 384), (17, 1, 256), (1, 3, 256), (40, 4, 1024)]
+# (positions, streams, hidden): GLM-5's 4 streams, fewer, and 5..8 (the wide kernels:
+# an 8 x 8 Sinkhorn layout and up to 80 projections)
+SHAPES = [(8, 4, 4096), (3, 4, 512), (5, 2, 384), (17, 1, 256), (1, 3, 256), (40, 4, 1024),
+          (4, 5, 512), (3, 6, 1024), (6, 8, 4096), (9, 7, 256)]
 
 
 @pytest.mark.parametrize("P,N,D", SHAPES)
@@ -116,14 +119,15 @@ def test_hc_prepare_glm5_scale_streams(oracle, dev):
 
 @pytest.mark.parametrize("eps", [1e-3, 0.05])
 @pytest.mark.parametrize("iters", [1, 3, 4, 20])
-def test_hc_prepare_large_eps_and_iteration_count(oracle, dev, eps, iters):
+@pytest.mark.parametrize("N", [4, 8])
+def test_hc_prepare_large_eps_and_iteration_count(oracle, dev, eps, iters, N):
     # At hc_eps 1e-6 a dropped eps (in the rsqrt, pre, the softmax or any Sinkhorn
     # denominator) moves post/comb by ~1e-6, inside the 2e-5 bound; at 1e-3 and 0.05 it
     # moves them by far more. The oracle's iteration count is pinned on the CPU, and 3 and 4
     # iterations differ by more than the bound for these logits, so matching it at each
     # count pins the device's count too.
-    P, N, D = 5, 4, 1024
-    fn, base, scale = make_site(90 + iters, N, D)
+    P, D = 5, 1024
+    fn, base, scale = make_site(90 + iters + N, N, D)
     base[2 * N:] = np.random.default_rng(91).uniform(-3, 3, size=N * N).astype(np.float32)
     st = streams_of(92, P, N, D)
     site = DeviceHcSite.from_numpy(fn, base, scale, N, iters, eps, dev)
@@ -134,11 +138,11 @@ def test_hc_prepare_large_eps_and_iteration_count(oracle, dev, eps, iters):
     check_f16(out, coll, ulps=1, extra=collapse_cond(st))
 
 
-@pytest.mark.parametrize("N", [1, 2, 3])
+@pytest.mark.parametrize("N", [1, 2, 3, 5, 6, 7])
 def test_hc_prepare_zero_eps_fewer_streams(oracle, dev, N):
-    # hc_mult below 4 leaves entries of the device's 4 x 4 Sinkhorn layout outside N x N;
-    # at hc_eps 0 their rows and columns sum to 0, and the reference (which has no such
-    # entries) stays finite: so must the device, and match the oracle
+    # hc_mult below 4 (or 5..7) leaves entries of the device's 4 x 4 (8 x 8) Sinkhorn
+    # layout outside N x N; at hc_eps 0 their rows and columns sum to 0, and the reference
+    # (which has no such entries) stays finite: so must the device, and match the oracle
     P, D = 3, 512
     fn, base, scale = make_site(300 + N, N, D)
     st = streams_of(301 + N, P, N, D)
@@ -176,7 +180,7 @@ def test_rms_norm_vs_oracle(oracle, dev, P, D):
     check_f16(y, oracle.rms_norm(x, w, NORM_EPS), ulps=2)
 
 
-@pytest.mark.parametrize("P,N,D", [(8, 4, 4096), (5, 3, 256), (2, 1, 130)])
+@pytest.mark.parametrize("P,N,D", [(8, 4, 4096), (5, 3, 256), (2, 1, 130), (4, 8, 512), (3, 6, 256)])
 def test_hc_mix_vs_oracle(oracle, dev, P, N, D):
     rng = np.random.default_rng(P * N + D)
     b = rng.normal(size=(P, D)).astype(np.float16).view(np.uint16)
@@ -213,9 +217,9 @@ def _block_layer(hidden, seed):
     return cfg, synth.make_layer(cfg, seed)
 
 
-@pytest.mark.parametrize("P", [1, 8, 37])
-def test_moe_block_equals_separate_calls(dev, P):
-    N, D = 4, 512
+@pytest.mark.parametrize("P,N", [(1, 4), (8, 4), (37, 4), (5, 8), (3, 6)])
+def test_moe_block_equals_separate_calls(dev, P, N):
+    D = 512
     cfg, layer = _block_layer(D, 31)
     d = DeviceMoeLayer(layer, dev)
     fn, base, scale = make_site(32, N, D)
@@ -235,11 +239,12 @@ def test_moe_block_equals_separate_calls(dev, P):
     d.close()
 
 
-def test_moe_block_vs_oracle_chain(oracle, dev):
+@pytest.mark.parametrize("N", [4, 8])
+def test_moe_block_vs_oracle_chain(oracle, dev, N):
     # oracle chain: hc_prepare -> rms_norm -> the MoE on the device's h and routing ->
     # hc_mix; the MoE part at the north-star bound, the final streams too
     from test_gpu_moe import check_out, check_routing, ocfg_of
-    P, N, D = 6, 4, 512
+    P, D = 6, 512
     cfg, layer = _block_layer(D, 41)
     d = DeviceMoeLayer(layer, dev)
     fn, base, scale = make_site(42, N, D)
@@ -293,9 +298,9 @@ def test_block_argument_errors(dev):
     st = torch.zeros(3, N, D, dtype=torch.float16, device=dev)
     with pytest.raises(_lib.Exl3Error, match="overlap"):
         moe_block(d, site, nw, NORM_EPS, st, out=st)
-    bad = DeviceHcSite(5, 20, EPS, site.fn, site.base, site.scale)
+    bad = DeviceHcSite(9, 20, EPS, site.fn, site.base, site.scale)
     with pytest.raises(_lib.Exl3Error, match="hc_mult"):
-        hc_prepare(torch.zeros(1, 5, D, dtype=torch.float16, device=dev), bad)
+        hc_prepare(torch.zeros(1, 9, D, dtype=torch.float16, device=dev), bad)
     odd = DeviceHcSite(3, 20, EPS, site.fn, site.base, site.scale)
     with pytest.raises(_lib.Exl3Error, match="multiple of 64"):
         hc_prepare(torch.zeros(1, 3, 200, dtype=torch.float16, device=dev), odd)
