@@ -590,6 +590,47 @@ def test_dispatch_many_pairs(oracle, dev, N):
     d.close()
 
 
+def test_dispatch_over_a_million_pairs(oracle, dev):
+    # 131,200 rows x top-8 = 1,049,600 pairs: 64 chunks of 17,408 pairs, 17 rounds of 64
+    # pairs per wave, so each wave takes its pairs' experts in two batches of loads (the
+    # 16-round batch, then one more). The rows repeat with period 4,100: the oracle routes
+    # the first 4,100, and every copy of a row must get that row's routing and, bit for
+    # bit, its output (a row's long-run output depends only on its own input), wherever
+    # its pairs fall among the chunks
+    cfg = synth.MoeConfig(hidden=256, inter=128, n_experts=64, top_k=8, routed_scaling_factor=2.0,
+                          shared_inter=128, gate_up_K=3, gate_up_cb=1, down_K=2, down_cb=2, shared_K=0)
+    layer, words = glm5_layer_on_device(dev, 62, "mill", cfg, [3, 17, 40], 0.3)
+    R, reps, H = 4100, 32, cfg.hidden
+    N = R * reps
+    base = synth.activations(62, "mill.x", R, H)
+    x = to_dev(np.tile(base, (reps, 1)), dev, N, 1, H)
+    d = DeviceMoeLayer(layer, dev, words=words)
+    d.diag_enable()
+    y = d(x).view(N, H)
+    _, ids = d.route(x)
+    ids = ids.cpu().numpy().reshape(N, -1)
+    assert (ids.reshape(reps, R, -1) == ids[None, :R]).all()
+    oc = ocfg_of(oracle, cfg, True)
+    idx, w, _ = check_routing(oracle, oracle.router_logits(base, layer.router_w), layer.bias, ids[:R], oc)
+    runs = oracle.moe_runs(np.tile(idx, (reps, 1)))
+    hist = {}
+    for r in runs["run_len"].tolist():
+        hist[min(r, 64)] = hist.get(min(r, 64), 0) + 1
+    assert d.diag()["run_hist"] == hist
+    check_diag_bytes(d.diag(), runs["run_len"], cfg, LONG_PASS_ROWS)
+    yc = y.cpu()
+    yr = yc.view(reps, R, H)
+    assert torch.equal(yr, yr[:1].expand(reps, R, H).contiguous())
+    rows = [0, 1, 2175, 2176, R // 2, R - 1]
+    for r in rows:
+        check_row_alone(d, x, yc, r, N)
+    used = set(idx[rows].reshape(-1).tolist())
+    want = oracle.moe_layer_routed(oc, oracle_experts(layer, words, used), oracle_shared(layer, words),
+                                   base[rows], idx[rows], w[rows])
+    check_out(yc[rows], want)
+    d.close()
+
+
 @pytest.mark.parametrize("gu_K,gu_cb,dn_K,dn_cb", [(1, 0, 2, 1), (2, 2, 3, 0), (3, 1, 6, 2), (5, 0, 7, 1),
                                                    (6, 2, 8, 0), (7, 1, 1, 2), (8, 0, 4, 1)])
 def test_layer_k_codebook_sweep(oracle, dev, gu_K, gu_cb, dn_K, dn_cb):
