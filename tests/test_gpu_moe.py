@@ -667,7 +667,9 @@ def test_layer_many_experts_grouped(oracle, dev):
     layer = synth.make_layer(cfg, 1024)
     d = DeviceMoeLayer(layer, dev)
     oc = ocfg_of(oracle, cfg, True)
-    for B in (3, 20):  # 48 pairs: one-wave dispatch; 320 pairs: workgroup counting sort
+    # 48 pairs: one-wave dispatch; 320 pairs: the one-workgroup counting sort; 2080 pairs:
+    # the counting sort over 3 workgroups (every expert's count read from each chunk)
+    for B in (3, 20, 130):
         h = synth.activations(1024, f"many.x.{B}", B, cfg.hidden)
         x = to_dev(h, dev, B, 1, cfg.hidden)
         d.diag_reset()
