@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 #include "exl3_device.hpp"
 #include "exl3_internal.hpp"
@@ -301,6 +302,21 @@ __device__ __forceinline__ void stage_part(__amdgpu_buffer_rsrc_t src, uint32_t 
   }
 }
 
+// Runs pass(std::integral_constant<int, NRB>) with NRB = the pass's occupied 16-row
+// blocks, (nr + 15) / 16 of the kLongBlocks: a short pass computes no MFMAs and reads no
+// A operands for its empty blocks (whose rows are never stored). Each block count is its
+// own copy of the pass, so the accumulators of the blocks it has are all it holds.
+template <typename F>
+__device__ __forceinline__ void with_blocks(int nr, F &&pass) {
+  static_assert(kLongBlocks == 4, "one case per block count");
+  switch ((nr + 15) >> 4) {
+    case 1: pass(std::integral_constant<int, 1>{}); break;
+    case 2: pass(std::integral_constant<int, 2>{}); break;
+    case 3: pass(std::integral_constant<int, 3>{}); break;
+    default: pass(std::integral_constant<int, 4>{});
+  }
+}
+
 // Work unit u of the long-run kernels: pass u of the dispatch's pass table, or (shared
 // mode) rows [u * kLongRows, u * kLongRows + kLongRows) of the trellis shared expert.
 __device__ __forceinline__ bool pass_info(const MoeArgs &a, int u, int shared_mode, RunInfo &ri) {
@@ -372,32 +388,40 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
     // in the staged k order)
     const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(a.xrot + ((int64_t)(ri.off + p0) * 2 + proj) * a.H), (short)0, (int)(nr * row_bytes), 0x00020000);
-    f32x4 D[kLongBlocks][2];
-    for (int sl = 0; sl < n_sl; ++sl) {
-      for (int pt = 0; pt < n_parts; ++pt) {
-        const int k0 = (sl * n_parts + pt) * part_k;
-        stage_part<kDup, kStageBatchGu>(src, row_bytes, 2u * k0, q_row, q_lg, nr, xs, xs_stride);
-        __syncthreads();
-        if (active)
-          qmv_slice_rb<K, CB, PD, kLongBlocks>(base, k_tiles, out / 16, k0 / 16, np, part, xs, xs_stride,
-                                               nr, slot, D, sl == 0 && pt == 0);
-        __syncthreads();
-      }
-    }
-    if (active) {
-      const int col = np * 32;
-#pragma unroll
-      for (int rb = 0; rb < kLongBlocks; ++rb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 16 * rb + d_row(i);
-          if (r < nr) {
-            float *y = a.yhat_gu + (int64_t)((ri.off + p0 + r) * 2 + proj) * n_sl * a.Imax + col;
-            y[d_col(0)] = D[rb][0][i];
-            y[d_col(1)] = D[rb][1][i];
-          }
+    with_blocks(nr, [&](auto nrb) {
+      constexpr int NRB = decltype(nrb)::value;
+      f32x4 D[NRB][2];
+      for (int sl = 0; sl < n_sl; ++sl) {
+        for (int pt = 0; pt < n_parts; ++pt) {
+          const int k0 = (sl * n_parts + pt) * part_k;
+          stage_part<kDup, kStageBatchGu>(src, row_bytes, 2u * k0, q_row, q_lg, nr, xs, xs_stride);
+          __syncthreads();
+          if (active)
+            qmv_slice_rb<K, CB, PD, NRB>(base, k_tiles, out / 16, k0 / 16, np, part, xs, xs_stride, nr, slot,
+                                         D, sl == 0 && pt == 0);
+          __syncthreads();
         }
-    }
+      }
+      if (active) {
+        const int col = np * 32;
+        // the lane's first row, read here (not hoisted out of the pass loop, where the
+        // rows of every block would each hold a VGPR through the decode)
+        int lr = threadIdx.x;
+        asm volatile("" : "+v"(lr));
+        lr = 4 * ((lr & 63) >> 4);
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * rb + lr + i;
+            if (r < nr) {
+              float *y = a.yhat_gu + (int64_t)((ri.off + p0 + r) * 2 + proj) * n_sl * a.Imax + col;
+              y[d_col(0)] = D[rb][0][i];
+              y[d_col(1)] = D[rb][1][i];
+            }
+          }
+      }
+    });
   }
 }
 
@@ -435,32 +459,40 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
     const int nr = min(kLongRows, ri.len - p0);
     const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(a.act + (int64_t)(ri.off + p0) * a.Imax), (short)0, (int)(nr * row_bytes), 0x00020000);
-    f32x4 D[kLongBlocks][2];
-    for (int sl = 0; sl < n_sl; ++sl) {
-      for (int pt = 0; pt < n_parts; ++pt) {
-        const int k0 = (sl * n_parts + pt) * part_k;
-        stage_part<kDup, kStageBatchDn>(src, row_bytes, 2u * k0, q_row, q_lg, nr, xs, xs_stride);
-        __syncthreads();
-        if (active)
-          qmv_slice_rb<K, CB, PD, kLongBlocks>(tb.tr[2], k_tiles, a.H / 16, k0 / 16, np, part, xs, xs_stride,
-                                               nr, slot, D, sl == 0 && pt == 0);
-        __syncthreads();
-      }
-    }
-    if (active) {
-      const int col = np * 32;
-#pragma unroll
-      for (int rb = 0; rb < kLongBlocks; ++rb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 16 * rb + d_row(i);
-          if (r < nr) {
-            float *y = a.yhat_dn + (int64_t)(ri.off + p0 + r) * a.S_dn * a.H + col;
-            y[d_col(0)] = D[rb][0][i];
-            y[d_col(1)] = D[rb][1][i];
-          }
+    with_blocks(nr, [&](auto nrb) {
+      constexpr int NRB = decltype(nrb)::value;
+      f32x4 D[NRB][2];
+      for (int sl = 0; sl < n_sl; ++sl) {
+        for (int pt = 0; pt < n_parts; ++pt) {
+          const int k0 = (sl * n_parts + pt) * part_k;
+          stage_part<kDup, kStageBatchDn>(src, row_bytes, 2u * k0, q_row, q_lg, nr, xs, xs_stride);
+          __syncthreads();
+          if (active)
+            qmv_slice_rb<K, CB, PD, NRB>(tb.tr[2], k_tiles, a.H / 16, k0 / 16, np, part, xs, xs_stride, nr,
+                                         slot, D, sl == 0 && pt == 0);
+          __syncthreads();
         }
-    }
+      }
+      if (active) {
+        const int col = np * 32;
+        // the lane's first row, read here (not hoisted out of the pass loop, where the
+        // rows of every block would each hold a VGPR through the decode)
+        int lr = threadIdx.x;
+        asm volatile("" : "+v"(lr));
+        lr = 4 * ((lr & 63) >> 4);
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * rb + lr + i;
+            if (r < nr) {
+              float *y = a.yhat_dn + (int64_t)(ri.off + p0 + r) * a.S_dn * a.H + col;
+              y[d_col(0)] = D[rb][0][i];
+              y[d_col(1)] = D[rb][1][i];
+            }
+          }
+      }
+    });
   }
 }
 

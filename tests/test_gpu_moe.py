@@ -183,6 +183,32 @@ def test_small_layer_vs_oracle(oracle, dev, B):
     d.close()
 
 
+def test_long_passes_every_block_count(oracle, dev):
+    # long-run calls (>= 65 rows) on configs[0]'s layer (16 experts, top-2): 100 rows give
+    # runs of 5-22 rows (passes of one or two 16-row MFMA blocks), 300 rows 27-53 (two to
+    # four blocks), 700 rows 66-132 (a full 64-row pass of four blocks, then a shorter
+    # one); each pass computes only its occupied blocks. Every row against the oracle.
+    cfg = synth.config_small()
+    layer = synth.make_layer(cfg, 2025)
+    d = DeviceMoeLayer(layer, dev)
+    oc = ocfg_of(oracle, cfg, False)
+    seen = set()
+    for B in (100, 300, 700):
+        h = synth.activations(2025, f"small.long.{B}", B, cfg.hidden)
+        x = to_dev(h, dev, B, 1, cfg.hidden)
+        y = d(x)
+        _, ids = d.route(x)
+        logits = oracle.router_logits(h, layer.router_w)
+        idx, w, _ = check_routing(oracle, logits, layer.bias, ids.cpu().numpy(), oc)
+        for ln in oracle.moe_runs(idx)["run_len"].tolist():
+            for p0 in range(0, ln, LONG_PASS_ROWS):
+                seen.add((min(LONG_PASS_ROWS, ln - p0) + 15) // 16)
+        want = oracle.moe_layer_routed(oc, [l.oracle_dict() for l in layer.experts], None, h, idx, w)
+        check_out(y, want)
+    assert seen == {1, 2, 3, 4}, seen
+    d.close()
+
+
 def test_layer_with_shared_experts(oracle, dev):
     # trellis shared expert (configs[4]'s mix, small) and an f16 shared expert
     for shared_K in (6, 0):
