@@ -50,8 +50,8 @@ struct alignas(16) RunRec {
 enum SharedKind { kSharedNone = 0, kSharedTrellis = 1, kSharedDense = 2 };
 
 // Everything a kernel of one layer call needs, passed by value.
-// Long-run mode (calls of more than 16 token rows): the expert kernels take passes of
-// up to kLongBlocks 16-row MFMA blocks per decode.
+// Long-run mode (calls of at least EXL3_MOE_LONG_ROWS token rows, 65 by default): the
+// expert kernels take passes of up to kLongBlocks 16-row MFMA blocks per decode.
 constexpr int kLongBlocks = 4;
 constexpr int kLongRows = 16 * kLongBlocks;
 
