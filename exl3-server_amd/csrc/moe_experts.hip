@@ -255,10 +255,10 @@ __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(kDnW
 // Long runs (calls of 65 token rows or more): 8-wave workgroups, wave w owns n-pair
 // 8*cb + w, passes of up to kLongRows rows with up to kLongBlocks 16-row MFMA blocks
 // per decode (qmv_slice_rb over the pass's occupied blocks only), and every k slice of
-// the tensor in one workgroup: each
-// block's accumulators run on from the first k step to the last (the reference's staged
-// path likewise sums in its own association, within 1% of max |value| of its QMV by its
-// test, glm5_gemv_nt_test.cpp:221-247). One partial per output goes to slice position 0.
+// the tensor in one workgroup: each block's accumulators run on from the first k step
+// to the last (the reference's staged path likewise sums in its own association, within
+// 1% of max |value| of its QMV by its test, glm5_gemv_nt_test.cpp:221-247). One partial
+// per output goes to slice position 0.
 using exl3m::kLongBlocks;
 using exl3m::kLongRows;
 constexpr int kLongThreads = 512;
