@@ -645,20 +645,89 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
         if (e < E && !s_keep[wave][e / gsize]) sfc[j] = -INFINITY;
       }
     }
-    // top_k by repeated wave argmax: largest sfc, ties to the lower expert id
-    uint32_t taken = 0;
+    // top_k: largest sfc, ties to the lower expert id. T = the K-th largest of the 64
+    // lanes' largest order keys, by a radix select over its bits (one ballot per bit): K
+    // lanes hold a key >= T, each a different expert, so the top K keys are all >= T.
+    // Those candidates (about K) go to LDS and each one ranks itself against all of
+    // them by the key above the complemented expert id: its rank is its pick index.
+    // More than 64 candidates (scores tied across many experts) take the repeated wave
+    // argmax below, which picks the same experts in the same order.
     float denom = 0.0f;
     float my_w = 0.0f;
     int my_id = 0;
-    for (int k = 0; k < K; ++k) {
+    uint32_t okey[kJ];
+    uint32_t lmax = 0;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int e = lane + 64 * j;
+      okey[j] = (j < jn && e < E) ? order_key(sfc[j]) : 0u;
+      lmax = max(lmax, okey[j]);
+    }
+    uint32_t thr = 0, decided = 0;
+    int need = K;
+#pragma unroll
+    for (int bit = 31; bit >= 0; --bit) {
+      // lanes that match the bits decided so far and have this bit set
+      const uint32_t t = 1u << bit;
+      const int c = __builtin_popcountll(__ballot((lmax & (decided | t)) == (thr | t)));
+      if (c >= need) {
+        thr |= t;
+      } else {
+        need -= c;
+      }
+      decided |= t;
+    }
+    uint64_t *cand = reinterpret_cast<uint64_t *>(&s_buf[wave][0]);  // 64 keys
+    float *cand_sc = &s_buf[wave][128];
+    int *pick_id = reinterpret_cast<int *>(&s_buf[wave][192]);
+    float *pick_sc = &s_buf[wave][256];
+    int n_c = 0;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const bool cj = okey[j] >= thr && okey[j] != 0u;
+      const uint64_t m = __ballot(cj);
+      const int pos = n_c + __builtin_popcountll(m & lanes_below());
+      if (cj && pos < 64) {
+        cand[pos] = ((uint64_t)okey[j] << 32) | (uint64_t)(~(uint32_t)(lane + 64 * j));
+        cand_sc[pos] = sc[j];
+      }
+      n_c += __builtin_popcountll(m);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (n_c <= 64) {
+      const uint64_t mine = lane < n_c ? cand[lane] : 0;
+      const float msc = lane < n_c ? cand_sc[lane] : 0.0f;
+      const uint32_t mh = (uint32_t)(mine >> 32), ml = (uint32_t)mine;
+      int rank = 0;
+      for (int i = 0; i < n_c; ++i) {
+        const uint32_t oh = (uint32_t)__builtin_amdgcn_readlane((int)mh, i);
+        const uint32_t ol = (uint32_t)__builtin_amdgcn_readlane((int)ml, i);
+        rank += (oh > mh || (oh == mh && ol > ml)) ? 1 : 0;
+      }
+      if (lane < n_c && rank < K) {
+        pick_id[rank] = (int)~ml;
+        pick_sc[rank] = msc;
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      if (lane < K) {
+        my_id = pick_id[lane];
+        my_w = pick_sc[lane];
+      }
+      // the weights' sum in pick order, as the argmax loop adds them
+      for (int k = 0; k < K; ++k)
+        denom += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), k));
+    }
+    uint32_t taken = 0;
+    for (int k = 0; k < (n_c <= 64 ? 0 : K); ++k) {
       uint32_t bkey = 0;
       int bj = 0;
       float bsc = 0.0f;
 #pragma unroll
       for (int j = 0; j < kJ; ++j) {
-        const int e = lane + 64 * j;
-        if (j < jn && e < E && !((taken >> j) & 1u)) {
-          const uint32_t key = order_key(sfc[j]);
+        if (!((taken >> j) & 1u)) {
+          const uint32_t key = okey[j];
           if (key > bkey) {
             bkey = key;
             bj = j;

@@ -144,6 +144,42 @@ def test_topk_route_known_answers(dev):
     assert sorted(ids[0].tolist()) == [0, 1]
 
 
+def _sigmoid_f32(x):
+    return (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+
+
+@pytest.mark.parametrize("E,K,levels", [(288, 8, 1), (288, 8, 3), (288, 8, 16), (288, 8, 60),
+                                        (16, 2, 2), (1024, 16, 24), (1024, 16, 200)])
+def test_topk_route_ties_to_lower_ids(dev, E, K, levels):
+    # scores drawn from a few levels (logits -1 .. 7, whose f32 sigmoids all differ), so
+    # many experts tie, also across the K-th place (glm5_moe.cpp:16-60: top_k by biased
+    # score, ties to the lower expert id); the ids in pick order and the weights (un-biased
+    # scores, normalised in pick order, scaled) against numpy. The first row ties every
+    # expert; the second puts 40 experts at logit 30, whose sigmoid rounds to exactly 1 in
+    # f32. Up to 16 levels put more than 64 experts at or above the K-th place's score.
+    rng = np.random.default_rng(E * 1000 + levels)
+    N = 24
+    lv = rng.integers(0, levels, size=(N, E))
+    lg = (lv.astype(np.float32) * np.float32(8.0 / levels) - np.float32(1.0)).astype(np.float32)
+    lg[0] = 0.5
+    lg[1, rng.choice(E, size=min(40, E), replace=False)] = 30.0
+    b = np.zeros(E, np.float32)
+    w, ids = moe_topk_route(torch.from_numpy(lg).to(dev), torch.from_numpy(b).to(dev), 1, 1, K,
+                            True, 2.5)
+    ids, w = ids.cpu().numpy(), w.cpu().numpy()
+    sig = _sigmoid_f32(lg)
+    assert sig[1].max() == 1.0 and (sig[1] == 1.0).sum() == min(40, E)
+    for r in range(N):
+        order = sorted(range(E), key=lambda e: (-sig[r, e], e))[:K]
+        assert ids[r].tolist() == order, (r, ids[r].tolist(), order)
+        sc = _sigmoid_f32(lg[r, order])
+        denom = np.float32(0.0)
+        for v in sc:
+            denom = np.float32(denom + v)
+        want = sc / (denom + np.float32(1e-20)) * np.float32(2.5)
+        assert np.allclose(w[r], want, rtol=2e-6, atol=0), (r, w[r], want)
+
+
 def test_topk_route_vs_oracle_many_rows(oracle, dev):
     rng = np.random.default_rng(3)
     E, K = 288, 8
