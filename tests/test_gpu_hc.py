@@ -217,8 +217,9 @@ def _block_layer(hidden, seed):
     return cfg, synth.make_layer(cfg, seed)
 
 
-@pytest.mark.parametrize("P,N", [(1, 4), (8, 4), (37, 4), (5, 8), (3, 6)])
+@pytest.mark.parametrize("P,N", [(1, 4), (8, 4), (37, 4), (5, 8), (3, 6), (100, 4), (70, 8)])
 def test_moe_block_equals_separate_calls(dev, P, N):
+    # P >= 65: the long-run kernels, whose combine variant carries the fused mix
     D = 512
     cfg, layer = _block_layer(D, 31)
     d = DeviceMoeLayer(layer, dev)
