@@ -546,7 +546,9 @@ __device__ void dispatch_wg(const MoeArgs &a, const int32_t *id_out, int g, int 
 template <int kJ>
 __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int32_t *id_out,
                                                     int mode) {
-  __shared__ float s_buf[16][kMaxE];  // group path: scores_for_choice per wave; dispatch: counts
+  // group path: scores_for_choice per wave; top-k: a wave's candidates (8-byte keys);
+  // dispatch: counts
+  __shared__ __align__(16) float s_buf[16][kMaxE];
   __shared__ int s_keep[16][64];
   __shared__ int s_small[64];         // the pairs' experts when P <= 64 (one-wave dispatch)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
