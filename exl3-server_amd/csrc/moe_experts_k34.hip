@@ -1,0 +1,14 @@
+// Expert kernel instantiations for codebook widths K = 3 and 4 (moe_experts.hpp), in a
+// translation unit of their own so that the widths compile in parallel.
+#include "moe_experts.hpp"
+
+namespace exl3h {
+
+exl3_status launch_expert_k34(int K, int cb, int pd, int which, dim3 ub, hipStream_t st, const MoeArgs &a,
+                              int shared_mode, int dense_arg) {
+  if (K == 3) return launch_expert_k<3>(cb, pd, which, ub, st, a, shared_mode, dense_arg);
+  if (K == 4) return launch_expert_k<4>(cb, pd, which, ub, st, a, shared_mode, dense_arg);
+  return fail(EXL3_ERR_INVALID, "K out of range");
+}
+
+}  // namespace exl3h

@@ -34,7 +34,10 @@ CFLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
-SOURCES = ["trellis_kernels.hip", "moe_experts.hip", "moe.hip", "api.hip", "loader.hip", "hc.hip"]
+# the expert kernels' instantiations are spread over moe_experts_k*.hip so that they compile
+# in parallel (the longest first)
+SOURCES = ["moe_experts_k78.hip", "moe_experts_k56.hip", "moe_experts_k34.hip", "moe_experts_k12.hip",
+           "trellis_kernels.hip", "moe_experts.hip", "moe.hip", "api.hip", "loader.hip", "hc.hip"]
 
 
 def _compile(src: str) -> str:
