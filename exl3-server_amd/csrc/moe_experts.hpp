@@ -324,6 +324,135 @@ __device__ __forceinline__ void with_blocks(int nr, F &&pass) {
   }
 }
 
+// Double-buffered staging for the reference form (plain rows, one f16 per k-element):
+// passes run in parts of up to kDbSteps wave steps, and part t + 1's rows are copied into
+// the other of two LDS buffers by the 16-byte direct-to-LDS buffer load (lane i's 16
+// bytes land at the row's LDS address + 16 i, no register holds them) while part t is
+// decoded: one barrier per part, and the ring-word stream runs over the whole k range
+// with no break at the part boundaries. The buffers are two objects, so that the
+// compiler's wait for a copy covers reads of its own buffer only. Every step meets the
+// same A operands and accumulators as in the single-buffered form, in the same order.
+constexpr int kDbSteps = 4;
+constexpr int kDbRowWords = kStepTiles * kDbSteps * 8 + 4;  // a part row + 4 words (bank offset)
+constexpr int kDbBufWords = kLongRows * kDbRowWords;
+static_assert(kLongThreads == 512, "eight waves copy a part's rows, wave + 8i");
+typedef __attribute__((address_space(3))) void lds_void_t;
+// The two part buffers: LDS of the plain-form long-run kernels only, the kernels that
+// reference them.
+__shared__ __align__(16) uint32_t g_db_a[kDbBufWords];
+__shared__ __align__(16) uint32_t g_db_b[kDbBufWords];
+
+// This wave's rows of a part (rows wave + 8i below nr): 16-byte chunks [0, q_row) of each
+// row from byte kbyte0 of the row, into buf.
+__device__ __forceinline__ void db_issue(__amdgpu_buffer_rsrc_t src, uint32_t row_bytes, uint32_t kbyte0,
+                                         int q_row, int nr, uint32_t *buf) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < kLongRows / 8; ++i) {
+    const int r = wave + 8 * i;
+    if (r < nr && lane < q_row)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_void_t *)(buf + r * kDbRowWords), 16,
+                                               (uint32_t)r * row_bytes + kbyte0 + 16u * (uint32_t)lane, 0, 0, 0);
+  }
+}
+
+// One pass of up to 16 * NRB rows (nr >= 1) of a plain-form tensor over its whole k range
+// into D (from zero): rows from src (row r at byte r * row_bytes, in the staged k order),
+// ring words of n-pair np from base; active = this wave has an n-pair (idle waves copy
+// rows and meet the barriers). Ends with a barrier, so the buffers are free afterwards.
+template <int K, int CB, int PD, int NRB, int kPart>
+__device__ __forceinline__ void long_pass_db_parts(const uint32_t *base, int k_tiles, int tiles_n, int np,
+                                                   bool active, __amdgpu_buffer_rsrc_t src, uint32_t row_bytes,
+                                                   int nr, u32x4 *slot, f32x4 (&D)[NRB][2], uint32_t *dbA,
+                                                   uint32_t *dbB) {
+  static_assert(!dup_cb(CB), "plain rows only");
+  static_assert(kPart <= kDbSteps && kPart % PD == 0, "part steps");
+  constexpr int kTw = tile_words(false);
+  const int total = k_tiles / kStepTiles;                   // wave steps over the k range
+  const int n_parts = total / kPart;
+  constexpr int q_row = kPart * kStepTiles * kTw / 4;       // 16-byte chunks of a part row
+  constexpr uint32_t part_bytes = 16u * q_row;
+  // part 0's copies before the stream's first loads: the copies of a part are always
+  // older than the ring loads in flight when the part's wait comes (below)
+  db_issue(src, row_bytes, 0, q_row, nr, dbA);
+  SliceStream<K, PD> S;
+  if (active) S.start(base, k_tiles, tiles_n, 0, np);
+  const StepLane sl = step_lane();
+  const int lane = threadIdx.x & 63;
+  const int wbase = (sl.kt * 2 + sl.nt) * 8 * K;
+  // block r's A operands: staged row 16r + l % 16 (rows past nr hold stale values: their
+  // MFMA rows are never stored, and an MFMA row depends on its own A row only), so the
+  // blocks' offsets differ by constants that fold into the LDS reads
+  const int xo0 = (lane & 15) * kDbRowWords + sl.kt * kTw;
+  int xo[NRB];
+#pragma unroll
+  for (int r = 0; r < NRB; ++r) {
+    xo[r] = xo0 + 16 * r * kDbRowWords;
+    D[r][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    D[r][1] = D[r][0];
+  }
+  // Loads complete in issue order. When part t's wait comes, a wave that decodes has
+  // exactly PD steps of ring loads in flight (PD * (K > 4 ? 2 : 1) loads), all issued
+  // after its copies of part t (at the start of part t - 1, or before the stream began):
+  // waiting until no more than those are outstanding completes the copies; an idle wave
+  // waits for everything. After the barrier every wave's copies of part t are in LDS, and
+  // no wave reads the other buffer (part t - 1) any more.
+  constexpr int kInFlight = PD * (K > 4 ? 2 : 1);
+  static_assert(kInFlight < 16, "vmcnt field");
+  auto run_part = [&](int t, uint32_t *cur, uint32_t *nxt) {
+    if (active)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | kInFlight);  // vmcnt(kInFlight), expcnt/lgkmcnt unchecked
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // The workgroup barrier without __syncthreads' fences, which count the copies as LDS
+    // writes and wait for every load in flight (vmcnt(0)), the ring words of the next
+    // steps included. The copies are complete by the wait above; this wave's LDS reads of
+    // the previous part have all been consumed by its MFMAs; the empty asm statements
+    // keep the compiler from moving memory operations across the barrier.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (t + 1 < n_parts) db_issue(src, row_bytes, (uint32_t)(t + 1) * part_bytes, q_row, nr, nxt);
+    if (active) {
+#pragma unroll
+      for (int sb = 0; sb < kPart; sb += PD) {
+#pragma unroll
+        for (int b = 0; b < PD; ++b) {
+          uint32_t W[K + 1];
+          step_words<K>(slot, wbase, sl.m, S.L[b], W);
+          // past the last step: lane offsets beyond the tensor (zeros, no memory access),
+          // so that every step issues the same loads
+          const int nx = t * kPart + sb + b + PD;
+          const bool past = nx >= total;
+          step_load<K>(S.rsrc, past ? S.vo0 + kPastEnd : S.vo0, past ? S.vo1 + kPastEnd : S.vo1,
+                       past ? 0u : S.so0 + (uint32_t)nx * S.step_bytes, S.L[b]);
+          mfma_step_rb<K, CB, NRB>(W, cur + (sb + b) * (kStepTiles * kTw), xo, D);
+        }
+      }
+    }
+  };
+  for (int t = 0; t < n_parts; t += 2) {
+    run_part(t, dbA, dbB);
+    if (t + 1 < n_parts) run_part(t + 1, dbB, dbA);
+  }
+  __syncthreads();
+}
+
+// Parts of 4 wave steps where they divide the k range, else of 2 (a tensor's k range is
+// a multiple of 128, 2 wave steps): a part's steps unrolled, so that the loads in flight
+// at each part's wait are known to the compiler as they are to the wait.
+template <int K, int CB, int PD, int NRB>
+__device__ __forceinline__ void long_pass_db(const uint32_t *base, int k_tiles, int tiles_n, int np, bool active,
+                                             __amdgpu_buffer_rsrc_t src, uint32_t row_bytes, int nr,
+                                             u32x4 *slot, f32x4 (&D)[NRB][2], uint32_t *dbA, uint32_t *dbB) {
+  if ((k_tiles / kStepTiles) % kDbSteps == 0)
+    long_pass_db_parts<K, CB, PD, NRB, kDbSteps>(base, k_tiles, tiles_n, np, active, src, row_bytes, nr, slot, D,
+                                                 dbA, dbB);
+  else
+    long_pass_db_parts<K, CB, PD, NRB, 2>(base, k_tiles, tiles_n, np, active, src, row_bytes, nr, slot, D, dbA,
+                                          dbB);
+}
+
 // Work unit u of the long-run kernels: pass u of the dispatch's pass table, or (shared
 // mode) rows [u * kLongRows, u * kLongRows + kLongRows) of the trellis shared expert.
 __device__ __forceinline__ bool pass_info(const MoeArgs &a, int u, int shared_mode, RunInfo &ri) {
@@ -376,15 +505,17 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   if (!pass_info(a, u, shared_mode, ri)) return;
   const exl3m::ExpertTab &tb = a.tab[ri.e];
   const uint32_t *base = tb.tr[proj];
-  const int wave = threadIdx.x >> 6;
+  // uniform across the wave: in a scalar register, so that branches on it are scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int np = cb * kWaves + wave;
   const bool active = np < n_np;  // idle waves still stage rows and meet the barriers
   constexpr bool kDup = dup_cb(CB);
   const int part = long_part_steps(k_tiles, kDup), n_parts = ss / part;
   const int part_k = kStepTiles * part * 16;
   const int xs_stride = long_row_words(k_tiles, kDup);
+  // plain rows: the double buffers are static, the dynamic LDS holds the slots only
   uint32_t *xs = smem;
-  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * slot_chunks(K);
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + (kDup ? kLongRows * xs_stride : 0)) + wave * slot_chunks(K);
 
   const int q_row = part_k / 8;  // 16-byte chunks of xrot per row and part (a power of two)
   const int q_lg = __builtin_ctz(q_row);
@@ -398,6 +529,10 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
     with_blocks(nr, [&](auto nrb) {
       constexpr int NRB = decltype(nrb)::value;
       f32x4 D[NRB][2];
+      if constexpr (!kDup) {
+        long_pass_db<K, CB, PD, NRB>(base, k_tiles, out / 16, np, active, src, row_bytes, nr, slot, D, g_db_a,
+                                     g_db_b);
+      } else
       for (int sl = 0; sl < n_sl; ++sl) {
         for (int pt = 0; pt < n_parts; ++pt) {
           const int k0 = (sl * n_parts + pt) * part_k;
@@ -449,7 +584,7 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   RunInfo ri;
   if (!pass_info(a, u, shared_mode, ri)) return;
   const exl3m::ExpertTab &tb = a.tab[ri.e];
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches
   const int np = cb * kWaves + wave;
   const bool active = np < n_np;
   constexpr bool kDup = dup_cb(CB);
@@ -458,8 +593,9 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
   const int xs_stride = long_row_words(k_tiles, kDup);
   const int q_row = part_k / 8;  // 16-byte chunks of act per row and part (a power of two)
   const int q_lg = __builtin_ctz(q_row);
+  // plain rows: the double buffers are static, the dynamic LDS holds the slots only
   uint32_t *xs = smem;
-  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + kLongRows * xs_stride) + wave * slot_chunks(K);
+  u32x4 *slot = reinterpret_cast<u32x4 *>(smem + (kDup ? kLongRows * xs_stride : 0)) + wave * slot_chunks(K);
 
   const uint32_t row_bytes = 2u * a.Imax;
   for (int p0 = 0; p0 < ri.len; p0 += kLongRows) {
@@ -469,6 +605,10 @@ __global__ __launch_bounds__(kLongThreads) __attribute__((amdgpu_waves_per_eu(4,
     with_blocks(nr, [&](auto nrb) {
       constexpr int NRB = decltype(nrb)::value;
       f32x4 D[NRB][2];
+      if constexpr (!kDup) {
+        long_pass_db<K, CB, PD, NRB>(tb.tr[2], k_tiles, a.H / 16, np, active, src, row_bytes, nr, slot, D,
+                                     g_db_a, g_db_b);
+      } else
       for (int sl = 0; sl < n_sl; ++sl) {
         for (int pt = 0; pt < n_parts; ++pt) {
           const int k0 = (sl * n_parts + pt) * part_k;
@@ -512,8 +652,11 @@ namespace exl3h {
 static size_t expert_lds(int in, int pass_rows, int waves, int K, int cb) {
   return (size_t)pass_rows * staged_row_words(in / 16, dup_cb(cb)) * 4 + (size_t)waves * slot_chunks(K) * 16;
 }
+// Long-run kernels: the staged rows (halves form; the plain form's double buffers are
+// static LDS), then one ring-word slot per wave.
 static size_t long_lds(int in, int K, int cb) {
-  return (size_t)kLongRows * long_row_words(in / 16, dup_cb(cb)) * 4 + (size_t)(kLongThreads / 64) * slot_chunks(K) * 16;
+  return (dup_cb(cb) ? (size_t)kLongRows * long_row_words(in / 16, true) * 4 : 0) +
+         (size_t)(kLongThreads / 64) * slot_chunks(K) * 16;
 }
 
 // Per kernel instantiation: the one-time LDS attribute, set under std::call_once so that
@@ -521,16 +664,23 @@ static size_t long_lds(int in, int K, int cb) {
 struct KernelAttr {
   std::once_flag once;
   hipError_t rc = hipSuccess;
+  size_t max_dynamic = 0;
 };
 
 template <typename Kern>
 static exl3_status launch_kernel(Kern k, dim3 blocks, unsigned threads, size_t lds, hipStream_t st,
                                  const MoeArgs &a, int shared_mode, int dense_blocks, KernelAttr &attr) {
-  // above the 64 KB default; leaves room for the kernels' static LDS
+  // dynamic LDS above the 64 KB default, up to what the kernel's static LDS leaves of a
+  // workgroup's 160 KB (at most 128 KB)
   std::call_once(attr.once, [&] {
-    attr.rc = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    hipFuncAttributes fa{};
+    attr.rc = hipFuncGetAttributes(&fa, (const void *)k);
+    if (attr.rc != hipSuccess) return;
+    attr.max_dynamic = std::min<size_t>(128 * 1024, 160 * 1024 - std::min<size_t>(fa.sharedSizeBytes, 160 * 1024));
+    attr.rc = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)attr.max_dynamic);
   });
   if (attr.rc != hipSuccess) return hip_check(attr.rc, "hipFuncSetAttribute");
+  if (lds > attr.max_dynamic) return fail(EXL3_ERR_UNSUPPORTED, "expert kernel LDS above the workgroup's share");
   k<<<blocks, threads, lds, st>>>(a, shared_mode, dense_blocks);
   return EXL3_OK;
 }
