@@ -330,8 +330,9 @@ __device__ __forceinline__ void with_blocks(int nr, F &&pass) {
 // bytes land at the row's LDS address + 16 i, no register holds them) while part t is
 // decoded: one barrier per part, and the ring-word stream runs over the whole k range
 // with no break at the part boundaries. The buffers are two objects, so that the
-// compiler's wait for a copy covers reads of its own buffer only. Every step meets the
-// same A operands and accumulators as in the single-buffered form, in the same order.
+// compiler, which tracks the copies, does not hold reads of one buffer back for the copy
+// into the other. Every step meets the same A operands and accumulators as in the
+// single-buffered form, in the same order.
 constexpr int kDbSteps = 4;
 constexpr int kDbRowWords = kStepTiles * kDbSteps * 8 + 4;  // a part row + 4 words (bank offset)
 constexpr int kDbBufWords = kLongRows * kDbRowWords;
