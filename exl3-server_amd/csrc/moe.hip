@@ -648,12 +648,13 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       }
     }
     // top_k: largest sfc, ties to the lower expert id. T = the K-th largest of the 64
-    // lanes' largest order keys, by a radix select over its bits (one ballot per bit): K
-    // lanes hold a key >= T, each a different expert, so the top K keys are all >= T.
-    // Those candidates (about K) go to LDS and each one ranks itself against all of
-    // them by the key above the complemented expert id: its rank is its pick index.
-    // More than 64 candidates (scores tied across many experts) take the repeated wave
-    // argmax below, which picks the same experts in the same order.
+    // lanes' largest order keys: every lane counts the lane maxima above its own (64
+    // broadcast LDS reads, independent of each other), and T is the smallest lane maximum
+    // with fewer than K above it. K lanes hold a key >= T, each a different expert, so
+    // the top K keys are all >= T. Those candidates (about K) go to LDS and each one ranks
+    // itself against all of them by the key above the complemented expert id: its rank
+    // is its pick index. More than 64 candidates (scores tied across many experts) take
+    // the repeated wave argmax below, which picks the same experts in the same order.
     float denom = 0.0f;
     float my_w = 0.0f;
     int my_id = 0;
@@ -665,20 +666,19 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
       okey[j] = (j < jn && e < E) ? order_key(sfc[j]) : 0u;
       lmax = max(lmax, okey[j]);
     }
-    uint32_t thr = 0, decided = 0;
-    int need = K;
+    uint32_t *lm = reinterpret_cast<uint32_t *>(&s_buf[wave][320]);
+    lm[lane] = lmax;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    int gt0 = 0, gt1 = 0, gt2 = 0, gt3 = 0;
 #pragma unroll
-    for (int bit = 31; bit >= 0; --bit) {
-      // lanes that match the bits decided so far and have this bit set
-      const uint32_t t = 1u << bit;
-      const int c = __builtin_popcountll(__ballot((lmax & (decided | t)) == (thr | t)));
-      if (c >= need) {
-        thr |= t;
-      } else {
-        need -= c;
-      }
-      decided |= t;
+    for (int i = 0; i < 64; i += 4) {
+      gt0 += lm[i] > lmax ? 1 : 0;
+      gt1 += lm[i + 1] > lmax ? 1 : 0;
+      gt2 += lm[i + 2] > lmax ? 1 : 0;
+      gt3 += lm[i + 3] > lmax ? 1 : 0;
     }
+    const uint32_t thr = wave_min_u32((gt0 + gt1) + (gt2 + gt3) < K ? lmax : 0xFFFFFFFFu);
     uint64_t *cand = reinterpret_cast<uint64_t *>(&s_buf[wave][0]);  // 64 keys
     float *cand_sc = &s_buf[wave][128];
     int *pick_id = reinterpret_cast<int *>(&s_buf[wave][192]);
@@ -700,15 +700,11 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
     if (n_c <= 64) {
       const uint64_t mine = lane < n_c ? cand[lane] : 0;
       const float msc = lane < n_c ? cand_sc[lane] : 0.0f;
-      const uint32_t mh = (uint32_t)(mine >> 32), ml = (uint32_t)mine;
+      // every candidate's key by a broadcast LDS read (independent reads, issued ahead)
       int rank = 0;
-      for (int i = 0; i < n_c; ++i) {
-        const uint32_t oh = (uint32_t)__builtin_amdgcn_readlane((int)mh, i);
-        const uint32_t ol = (uint32_t)__builtin_amdgcn_readlane((int)ml, i);
-        rank += (oh > mh || (oh == mh && ol > ml)) ? 1 : 0;
-      }
+      for (int i = 0; i < n_c; ++i) rank += cand[i] > mine ? 1 : 0;
       if (lane < n_c && rank < K) {
-        pick_id[rank] = (int)~ml;
+        pick_id[rank] = (int)~(uint32_t)mine;
         pick_sc[rank] = msc;
       }
       __builtin_amdgcn_wave_barrier();
@@ -718,8 +714,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(MoeArgs a, float *w_out, int
         my_w = pick_sc[lane];
       }
       // the weights' sum in pick order, as the argmax loop adds them
-      for (int k = 0; k < K; ++k)
-        denom += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), k));
+      for (int k = 0; k < K; ++k) denom += pick_sc[k];
     }
     uint32_t taken = 0;
     for (int k = 0; k < (n_c <= 64 ? 0 : K); ++k) {
