@@ -149,7 +149,8 @@ def _sigmoid_f32(x):
 
 
 @pytest.mark.parametrize("E,K,levels", [(288, 8, 1), (288, 8, 3), (288, 8, 16), (288, 8, 60),
-                                        (16, 2, 2), (1024, 16, 24), (1024, 16, 200)])
+                                        (16, 2, 2), (1024, 16, 24), (1024, 16, 200),
+                                        (64, 64, 3), (40, 40, 2), (100, 64, 5), (130, 1, 1)])
 def test_topk_route_ties_to_lower_ids(dev, E, K, levels):
     # scores drawn from a few levels (logits -1 .. 7, whose f32 sigmoids all differ), so
     # many experts tie, also across the K-th place (glm5_moe.cpp:16-60: top_k by biased
@@ -157,6 +158,8 @@ def test_topk_route_ties_to_lower_ids(dev, E, K, levels):
     # scores, normalised in pick order, scaled) against numpy. The first row ties every
     # expert; the second puts 40 experts at logit 30, whose sigmoid rounds to exactly 1 in
     # f32. Up to 16 levels put more than 64 experts at or above the K-th place's score.
+    # K = E (every expert picked), K = 64 (the largest top-k) and K = 1 over full ties
+    # take the threshold's edge cases.
     rng = np.random.default_rng(E * 1000 + levels)
     N = 24
     lv = rng.integers(0, levels, size=(N, E))
