@@ -8,12 +8,13 @@
 //                 x . fn[j] (fn stored (W, N*D), as the reference's F.linear weight);
 //                 f32 partials per chunk. Each wave keeps its projections' fn slice in
 //                 registers and reuses it for every position of the group.
-//  k_hc_finalize  one workgroup per position: the partials summed in chunk order, the RMS
-//                 factor (w = rms * x.fn, the fused reference kernel's per-term product
-//                 folded out of the sum), pre/post/comb with the softmax over the last
-//                 axis, the Sinkhorn in the reference's loop order (glm5_hc.cpp:321-324),
-//                 the collapsed stream sum_n pre[n] * streams[n] rounded to f16, and,
-//                 given a norm weight, the RMSNorm of that row fused behind it.
+//  k_hc_finalize  two workgroups per position, side by side: both sum the partials in
+//                 chunk order and take the RMS factor (w = rms * x.fn, the fused
+//                 reference kernel's per-term product folded out of the sum); one forms
+//                 pre and the collapsed stream sum_n pre[n] * streams[n] rounded to f16
+//                 (and, given a norm weight, the RMSNorm of that row fused behind it),
+//                 the other post and comb, with the softmax over the last axis and the
+//                 Sinkhorn in the reference's loop order (glm5_hc.cpp:321-324).
 //  k_rms_norm     the RMSNorm alone, one workgroup per row.
 //  k_hc_mix       post[n] * out + comb^T @ residual in f16 (also fused into the MoE
 //                 combine, which then writes the new streams directly).
@@ -174,14 +175,17 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
   __shared__ float grp[S::kG][S::kJ];
   __shared__ float pre[kN];
   __shared__ float red[4];
-  const int64_t p = blockIdx.x;
+  // workgroup 2p: pre and the collapsed stream of position p; 2p + 1: post and comb (the
+  // latency-bound Sinkhorn of one wave runs beside the collapse and its norm)
+  const int64_t p = blockIdx.x >> 1;
+  const bool collapse = (blockIdx.x & 1) == 0;
   const int64_t ND = (int64_t)N * D;
   const int t = threadIdx.x;
   // the row's stream pairs, in flight while the projections are finished (the narrow
   // variant; the wide one loads each stream at the collapse, to keep its registers)
   const uint16_t *srow = streams + p * ND;
   uint32_t sp[kNarrow ? kN : 1][kHcPairs];
-  if constexpr (kNarrow) {
+  if (kNarrow && collapse) {
 #pragma unroll
     for (int n = 0; n < kN; ++n)
 #pragma unroll
@@ -192,7 +196,7 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
   // the norm weights too (the row's own streams stand in when there is no norm: same
   // length, never used)
   uint32_t wv[kHcPairs];
-  load_pairs(norm_w ? norm_w : srow, D, wv);
+  if (collapse) load_pairs(norm_w ? norm_w : srow, D, wv);
   // the chunk partials: thread (g, j) sums value j over chunks g, g + kG, ... in order
   // (their loads in flight together), then value j is the sum of the kG group sums in
   // group order
@@ -227,37 +231,43 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
     // (columns)
     const float rms = 1.0f / sqrtf(vals[S::kMaxW] / (float)ND + eps);
     const int lane = t;
-    if (lane < N) {
-      const float wp = vals[lane] * rms, wq = vals[N + lane] * rms;
-      pre[lane] = 1.0f / (1.0f + expf(-(wp * scale[0] + base[lane]))) + eps;
-      post_out[p * N + lane] = 2.0f * (1.0f / (1.0f + expf(-(wq * scale[1] + base[N + lane]))));
-    }
-    const int ci = lane >> 3, cj = lane & 7;
-    const bool live = ci < N && cj < N;
-    auto row_sum = [&](float v) {
-      const float s = v + xor_lanes<1>(v);
-      const float s2 = s + xor_lanes<2>(s);
-      return s2 + xor_lanes<4>(s2);
-    };
-    auto col_sum = [&](float v) {
-      const float s = v + xor_lanes<8>(v);
-      const float s2 = s + xor_lanes<16>(s);
-      return s2 + xor_lanes<32>(s2);
-    };
-    const float z = live ? vals[2 * N + ci * N + cj] * rms * scale[2] + base[2 * N + ci * N + cj] : -INFINITY;
-    float m = fmaxf(z, xor_lanes<1>(z));
-    m = fmaxf(m, xor_lanes<2>(m));
-    m = fmaxf(m, xor_lanes<4>(m));
-    float c = live ? expf(z - m) : 0.0f;
-    const float rs = row_sum(c);
-    c = live ? c / rs + eps : 0.0f;
-    auto norm = [&](float v, float sum) { return live ? v / (sum + eps) : 0.0f; };
-    c = norm(c, col_sum(c));
-    for (int it = 0; it < iters - 1; ++it) {
-      c = norm(c, row_sum(c));
+    if (collapse) {
+      if (lane < N) {
+        const float wp = vals[lane] * rms;
+        pre[lane] = 1.0f / (1.0f + expf(-(wp * scale[0] + base[lane]))) + eps;
+      }
+    } else {
+      if (lane < N) {
+        const float wq = vals[N + lane] * rms;
+        post_out[p * N + lane] = 2.0f * (1.0f / (1.0f + expf(-(wq * scale[1] + base[N + lane]))));
+      }
+      const int ci = lane >> 3, cj = lane & 7;
+      const bool live = ci < N && cj < N;
+      auto row_sum = [&](float v) {
+        const float s = v + xor_lanes<1>(v);
+        const float s2 = s + xor_lanes<2>(s);
+        return s2 + xor_lanes<4>(s2);
+      };
+      auto col_sum = [&](float v) {
+        const float s = v + xor_lanes<8>(v);
+        const float s2 = s + xor_lanes<16>(s);
+        return s2 + xor_lanes<32>(s2);
+      };
+      const float z = live ? vals[2 * N + ci * N + cj] * rms * scale[2] + base[2 * N + ci * N + cj] : -INFINITY;
+      float m = fmaxf(z, xor_lanes<1>(z));
+      m = fmaxf(m, xor_lanes<2>(m));
+      m = fmaxf(m, xor_lanes<4>(m));
+      float c = live ? expf(z - m) : 0.0f;
+      const float rs = row_sum(c);
+      c = live ? c / rs + eps : 0.0f;
+      auto norm = [&](float v, float sum) { return live ? v / (sum + eps) : 0.0f; };
       c = norm(c, col_sum(c));
+      for (int it = 0; it < iters - 1; ++it) {
+        c = norm(c, row_sum(c));
+        c = norm(c, col_sum(c));
+      }
+      if (live) comb_out[p * N * N + ci * N + cj] = c;
     }
-    if (live) comb_out[p * N * N + ci * N + cj] = c;
   }
   if (t < 64 && kNarrow) {
     // wave 0: lane l < 16 holds comb entry (l / 4, l % 4) of a 4 x 4 layout (entries
@@ -266,47 +276,54 @@ __global__ __launch_bounds__(256) void k_hc_finalize(const uint16_t *__restrict_
     // no LDS round trip per reduction
     const float rms = 1.0f / sqrtf(vals[S::kMaxW] / (float)ND + eps);
     const int lane = t;
-    if (lane < N) {
-      const float wp = vals[lane] * rms, wq = vals[N + lane] * rms;
-      pre[lane] = 1.0f / (1.0f + expf(-(wp * scale[0] + base[lane]))) + eps;
-      post_out[p * N + lane] = 2.0f * (1.0f / (1.0f + expf(-(wq * scale[1] + base[N + lane]))));
-    }
-    const int ci = (lane >> 2) & 3, cj = lane & 3;
-    const bool live = lane < 16 && ci < N && cj < N;
-    auto dpp = [](float v, auto ctrl) {
-      return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), decltype(ctrl)::value,
-                                                                 0xF, 0xF, false));
-    };
-    using X1 = std::integral_constant<int, 0xB1>;   // lane ^ 1
-    using X2 = std::integral_constant<int, 0x4E>;   // lane ^ 2
-    using R4 = std::integral_constant<int, 0x124>;  // rotate right by 4 within 16 lanes
-    using R8 = std::integral_constant<int, 0x128>;  // rotate right by 8 within 16 lanes
-    auto row_sum = [&](float v) {
-      const float s = v + dpp(v, X1{});
-      return s + dpp(s, X2{});
-    };
-    auto col_sum = [&](float v) {
-      const float s = v + dpp(v, R4{});
-      return s + dpp(s, R8{});
-    };
-    // softmax over the last axis (j), then + eps
-    const float z = live ? vals[2 * N + ci * N + cj] * rms * scale[2] + base[2 * N + ci * N + cj] : -INFINITY;
-    float m = fmaxf(z, dpp(z, X1{}));
-    m = fmaxf(m, dpp(m, X2{}));
-    float c = live ? expf(z - m) : 0.0f;
-    const float rs = row_sum(c);
-    c = live ? c / rs + eps : 0.0f;
-    // Sinkhorn: columns, then (iters - 1) x (rows, columns); the entries outside N x N
-    // are set to 0 at every step (a padded row or column sums to 0, so at eps = 0 its
-    // own division would be 0 / 0; the sums themselves run on every lane for the DPP)
-    auto norm = [&](float v, float sum) { return live ? v / (sum + eps) : 0.0f; };
-    c = norm(c, col_sum(c));
-    for (int it = 0; it < iters - 1; ++it) {
-      c = norm(c, row_sum(c));
+    if (collapse) {
+      if (lane < N) {
+        const float wp = vals[lane] * rms;
+        pre[lane] = 1.0f / (1.0f + expf(-(wp * scale[0] + base[lane]))) + eps;
+      }
+    } else {
+      if (lane < N) {
+        const float wq = vals[N + lane] * rms;
+        post_out[p * N + lane] = 2.0f * (1.0f / (1.0f + expf(-(wq * scale[1] + base[N + lane]))));
+      }
+      const int ci = (lane >> 2) & 3, cj = lane & 3;
+      const bool live = lane < 16 && ci < N && cj < N;
+      auto dpp = [](float v, auto ctrl) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), decltype(ctrl)::value,
+                                                                   0xF, 0xF, false));
+      };
+      using X1 = std::integral_constant<int, 0xB1>;   // lane ^ 1
+      using X2 = std::integral_constant<int, 0x4E>;   // lane ^ 2
+      using R4 = std::integral_constant<int, 0x124>;  // rotate right by 4 within 16 lanes
+      using R8 = std::integral_constant<int, 0x128>;  // rotate right by 8 within 16 lanes
+      auto row_sum = [&](float v) {
+        const float s = v + dpp(v, X1{});
+        return s + dpp(s, X2{});
+      };
+      auto col_sum = [&](float v) {
+        const float s = v + dpp(v, R4{});
+        return s + dpp(s, R8{});
+      };
+      // softmax over the last axis (j), then + eps
+      const float z = live ? vals[2 * N + ci * N + cj] * rms * scale[2] + base[2 * N + ci * N + cj] : -INFINITY;
+      float m = fmaxf(z, dpp(z, X1{}));
+      m = fmaxf(m, dpp(m, X2{}));
+      float c = live ? expf(z - m) : 0.0f;
+      const float rs = row_sum(c);
+      c = live ? c / rs + eps : 0.0f;
+      // Sinkhorn: columns, then (iters - 1) x (rows, columns); the entries outside N x N
+      // are set to 0 at every step (a padded row or column sums to 0, so at eps = 0 its
+      // own division would be 0 / 0; the sums themselves run on every lane for the DPP)
+      auto norm = [&](float v, float sum) { return live ? v / (sum + eps) : 0.0f; };
       c = norm(c, col_sum(c));
+      for (int it = 0; it < iters - 1; ++it) {
+        c = norm(c, row_sum(c));
+        c = norm(c, col_sum(c));
+      }
+      if (live) comb_out[p * N * N + ci * N + cj] = c;
     }
-    if (live) comb_out[p * N * N + ci * N + cj] = c;
   }
+  if (!collapse) return;
   __syncthreads();
   // collapsed = sum_n pre[n] * streams[n], in f16
   float x0[kHcPairs], x1[kHcPairs];
@@ -410,7 +427,7 @@ static void hc_prepare_go(const exl3_hc_site *hc, const uint16_t *streams, int64
                           float *part, hipStream_t st) {
   const int N = hc->mult, W = (2 + N) * N, ND = N * D, n_chunks = ND / kHcChunk;
   k_hc_proj<kN><<<dim3((unsigned)n_chunks, (unsigned)groups), 256, 0, st>>>(streams, P, ND, W, hc->fn, part);
-  k_hc_finalize<kN><<<(unsigned)P, 256, 0, st>>>(streams, N, D, W, n_chunks, part, hc->base, hc->scale,
+  k_hc_finalize<kN><<<(unsigned)(2 * P), 256, 0, st>>>(streams, N, D, W, n_chunks, part, hc->base, hc->scale,
                                                   hc->sinkhorn_iters, hc->eps, norm_w, norm_eps, out, post, comb);
 }
 
