@@ -34,6 +34,7 @@ using namespace exl3d;
 namespace {
 
 constexpr int kHcMaxN = 8;                       // streams (W <= 80)
+static_assert(kHcMaxN <= exl3m::kHcMixMax, "the mix's residual registers");
 constexpr int kHcNarrowN = 4;                    // the narrow kernels' streams (W <= 24; GLM-5's 4)
 constexpr int kHcChunk = 64;                     // elements of the N*D axis per workgroup
 
@@ -399,7 +400,9 @@ __global__ __launch_bounds__(256) void k_hc_mix(const uint16_t *__restrict__ bou
   const int64_t p = g / half_d;
   const int d = (int)(g % half_d) * 2;
   const uint32_t b = *reinterpret_cast<const uint32_t *>(bout + p * D + d);
-  exl3m::hc_mix_pair(post + p * N, comb + p * N * N, res + p * N * D + d, D, N, h2f(b & 0xffff), h2f(b >> 16),
+  uint32_t rv[exl3m::kHcMixMax];
+  exl3m::hc_mix_res(res + p * N * D + d, D, N, rv);
+  exl3m::hc_mix_pair(post + p * N, comb + p * N * N, rv, D, N, h2f(b & 0xffff), h2f(b >> 16),
                      out + p * N * D + d);
 }
 

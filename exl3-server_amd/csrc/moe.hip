@@ -844,6 +844,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFold ? 7 :
     for (int q = 0; q < 4; ++q) dsh[q] = pd[q];
   };
   if (!kFold && a.shared_kind == exl3m::kSharedDense) load_dsh();
+  // the mix's residual pairs (its only per-lane inputs), in flight with the rest (the
+  // folded form, held to 72 VGPRs, loads them at the mix)
+  uint32_t rv[exl3m::kHcMixMax];
+  if (!kFold && a.hc_out) exl3m::hc_mix_res(a.hc_res + (int64_t)row * a.hc_n * a.H + c, a.H, a.hc_n, rv);
   float r0 = 0.0f, r1 = 0.0f;
   for (int k0 = 0; k0 < a.topk; k0 += kCombineBatch) {
     const int nk = min(kCombineBatch, a.topk - k0);
@@ -951,8 +955,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFold ? 7 :
   if (a.hc_out) {
     // the hyper-connection mix behind the layer (g5_hc_mix), on the f16 output
     const int64_t so = (int64_t)row * a.hc_n * a.H + c;
-    exl3m::hc_mix_pair(a.hc_post + (int64_t)row * a.hc_n, a.hc_comb + (int64_t)row * a.hc_n * a.hc_n,
-                       a.hc_res + so, a.H, a.hc_n, lo16(o), hi16(o), a.hc_out + so);
+    if (kFold) exl3m::hc_mix_res(a.hc_res + so, a.H, a.hc_n, rv);
+    exl3m::hc_mix_pair(a.hc_post + (int64_t)row * a.hc_n, a.hc_comb + (int64_t)row * a.hc_n * a.hc_n, rv,
+                       a.H, a.hc_n, lo16(o), hi16(o), a.hc_out + so);
   }
 }
 

@@ -127,20 +127,28 @@ struct MoeArgs {
 // stream n, f16(f16(f16(post[n]) * b) + f16(sum_m f16(comb[m][n]) * residual[m])), the
 // f16 products exact in f32 and the sum over m accumulated in f32 (a matmul's).
 // res / out point at element d of stream 0; streams are D elements apart.
-__device__ __forceinline__ void hc_mix_pair(const float *post, const float *comb, const uint16_t *res, int D, int N,
-                                            float b0, float b1, uint16_t *out) {
+// The residual pairs are loaded once, up front (hc_mix_res), so that a caller can issue
+// them long before the mix: rv[m] = stream m's pair, m < N <= kHcMixMax.
+constexpr int kHcMixMax = 8;
+__device__ __forceinline__ void hc_mix_res(const uint16_t *res, int D, int N, uint32_t (&rv)[kHcMixMax]) {
+#pragma unroll
+  for (int m = 0; m < kHcMixMax; ++m) rv[m] = *reinterpret_cast<const uint32_t *>(res + (int64_t)min(m, N - 1) * D);
+}
+__device__ __forceinline__ void hc_mix_pair(const float *post, const float *comb, const uint32_t (&rv)[kHcMixMax],
+                                            int D, int N, float b0, float b1, uint16_t *out) {
   using exl3d::to_f16;
   auto h2f = [](uint32_t v) { return exl3d::f16_to_f32((uint16_t)v); };
   for (int n = 0; n < N; ++n) {
     const float pn = (float)to_f16(post[n]);
     const float a0 = (float)to_f16(pn * b0), a1 = (float)to_f16(pn * b1);
     float r0 = 0.0f, r1 = 0.0f;
-    for (int m = 0; m < N; ++m) {
-      const float cm = (float)to_f16(comb[m * N + n]);
-      const uint32_t rv = *reinterpret_cast<const uint32_t *>(res + (int64_t)m * D);
-      r0 = fmaf(cm, h2f(rv & 0xffffu), r0);
-      r1 = fmaf(cm, h2f(rv >> 16), r1);
-    }
+#pragma unroll
+    for (int m = 0; m < kHcMixMax; ++m)
+      if (m < N) {
+        const float cm = (float)to_f16(comb[m * N + n]);
+        r0 = fmaf(cm, h2f(rv[m] & 0xffffu), r0);
+        r1 = fmaf(cm, h2f(rv[m] >> 16), r1);
+      }
     const float o0 = a0 + (float)to_f16(r0), o1 = a1 + (float)to_f16(r1);
     *reinterpret_cast<uint32_t *>(out + (int64_t)n * D) =
         (uint32_t)exl3d::bitcast<uint16_t>(to_f16(o0)) | ((uint32_t)exl3d::bitcast<uint16_t>(to_f16(o1)) << 16);
