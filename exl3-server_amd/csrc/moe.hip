@@ -828,7 +828,7 @@ template <bool kFold>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFold ? 7 : 1))) void k_moe_combine(MoeArgs a) {
   const int lane = threadIdx.x & 63;
   const int n_cb = a.H / 128;
-  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t gw = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (gw >= (int64_t)a.N * n_cb) return;
   const int row = (int)(gw / n_cb), cb = (int)(gw % n_cb);
   const int c = cb * 128 + 2 * lane;
@@ -1912,7 +1912,9 @@ exl3_status moe_layer_run(exl3_moe_layer_t layer, const uint16_t *h, int64_t N, 
   if (a.fold)
     k_moe_combine<true><<<(unsigned)((N * (H / 128) + 3) / 4), 256, 0, st>>>(a);
   else
-    k_moe_combine<false><<<(unsigned)((N * (H / 128) + 3) / 4), 256, 0, st>>>(a);
+    // one wave per workgroup: the waves' loads spread over every CU (5.48 -> 5.11 us at
+    // B=8 against four-wave workgroups)
+    k_moe_combine<false><<<(unsigned)(N * (H / 128)), 64, 0, st>>>(a);
   EXL3_LAUNCHED("k_moe_combine");
   if (timed) {
     EXL3_HIP(hipEventRecord(layer->ev[4], st));
